@@ -1,0 +1,223 @@
+"""Quantized-linear benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--no-graph]
+
+A step is one quantized matmul (qmm_quantized_matmul through the C ABI) over
+one batch of synthetic input resident in HBM.  The default workload is the
+nvfp4 fused gate+up decode GEMV (M=1, N=34816, K=5120): the metric is achieved
+HBM GB/s over the algorithmic bytes (every weight, scale, input and output
+byte counted once).  Timed calls rotate over distinct weight copies totalling
+at least 512 MiB so each call reads weights from HBM, not the 256 MB
+Infinity Cache.  Steps are captured in a HIP graph and replayed (one replay =
+exactly K launches), bracketed by HIP events on the launch stream.
+
+Prints ONE JSON line on stdout.  The CPU baseline is the oracle's
+fp32-accumulating restatement, timed on the host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "oracle", ROOT / "mlx-runner_amd"):
+    sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"fp8": 5000.0, "bf16": 2500.0}
+
+CONFIGS = {
+    "mxfp8_gemv": dict(mode="mxfp8", M=1, N=5120, K=5120, xscale=1.0,
+                       workload="mxfp8 GEMV, x bf16 [1,5120], W [5120,5120]"),
+    "gateup": dict(mode="nvfp4", M=1, N=34816, K=5120, xscale=1.0,
+                   workload="nvfp4 fused gate+up decode GEMV, x bf16 [1,5120], W [34816,5120]"),
+    "down_m1": dict(mode="nvfp4", M=1, N=5120, K=17408, xscale=0.5,
+                    workload="nvfp4 down-proj skinny GEMM, x bf16 [1,17408], W [5120,17408]"),
+    "down_m2": dict(mode="nvfp4", M=2, N=5120, K=17408, xscale=0.5,
+                    workload="nvfp4 down-proj skinny GEMM, x bf16 [2,17408], W [5120,17408]"),
+    "down_m3": dict(mode="nvfp4", M=3, N=5120, K=17408, xscale=0.5,
+                    workload="nvfp4 down-proj skinny GEMM, x bf16 [3,17408], W [5120,17408]"),
+    "prefill": dict(mode="mxfp8", M=4096, N=17408, K=5120, xscale=1.0,
+                    workload="mxfp8 prefill GEMM, x bf16 [4096,5120], W [17408,5120]"),
+    "lmhead": dict(mode="nvfp4", M=1, N=248320, K=5120, xscale=1.0,
+                   workload="nvfp4 lm_head decode GEMV, x bf16 [1,5120], W [248320,5120]"),
+    "lmhead_prefill": dict(mode="nvfp4", M=2048, N=248320, K=5120, xscale=1.0,
+                           workload="nvfp4 lm_head prefill GEMM, x bf16 [2048,5120], W [248320,5120]"),
+}
+DEFAULT = "gateup"
+BITS = {"mxfp8": 8, "nvfp4": 4}
+GROUP = {"mxfp8": 32, "nvfp4": 16}
+ROTATE_BYTES = 512 << 20
+
+
+def algorithmic(cfg):
+    M, N, K, mode = cfg["M"], cfg["N"], cfg["K"], cfg["mode"]
+    wbytes = N * K * BITS[mode] // 8
+    sbytes = N * K // GROUP[mode]
+    return dict(w=wbytes, s=sbytes, bytes=wbytes + sbytes + M * K * 2 + M * N * 2, flops=2 * M * N * K)
+
+
+def roofline_of(cfg, alg, sec_per_call):
+    if cfg["M"] <= 8:
+        achieved = alg["bytes"] / sec_per_call / 1e9
+        return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(achieved / HBM_PEAK_GBS, 4))
+    achieved = alg["flops"] / sec_per_call / 1e12
+    peak = MFMA_PEAK_TFLOPS["fp8" if cfg["mode"] == "mxfp8" else "bf16"]
+    return dict(bound="mfma", achieved=round(achieved, 1), peak=peak, unit="TFLOP/s", frac=round(achieved / peak, 4))
+
+
+def traffic_from_profiles(name):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary, if one exists."""
+    for p in (ROOT / "profiles").glob(f"*{name}*pmc*.md"):
+        m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+        if m:
+            return float(m.group(1))
+    return None
+
+
+def cpu_baseline(cfg, xb, wq, s, budget_s=12.0):
+    """Oracle's fp32-accumulating qmm on host threads over a bounded sample of the workload."""
+    import numpy as np
+
+    import oracle as O
+
+    threads = min(16, os.cpu_count() or 1)
+    M, N, K = cfg["M"], cfg["N"], cfg["K"]
+    rows = N
+    # for the compute-bound configs take a slice of output columns (full K, all M rows)
+    if M > 8:
+        rows = max(64, min(N, int(N * 0.004)))
+    w_s, s_s = wq[:rows], s[:rows]
+    t0 = time.perf_counter()
+    O.qmm(cfg["mode"], xb, w_s, s_s, f32acc=True, threads=threads)
+    one = time.perf_counter() - t0
+    reps = max(1, min(1000, int(budget_s / max(one, 1e-6))))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        O.qmm(cfg["mode"], xb, w_s, s_s, f32acc=True, threads=threads)
+    dt = (time.perf_counter() - t0) / reps
+    sample_cfg = dict(cfg, N=rows)
+    alg = algorithmic(sample_cfg)
+    if M <= 8:
+        value, unit = alg["bytes"] / dt / 1e9, "GB/s"
+    else:
+        value, unit = alg["flops"] / dt / 1e12, "TFLOP/s"
+    sample = (f"{reps} calls of M={M} x {rows} of {N} output rows, K={K} ({cfg['mode']}), "
+              f"{dt * 1e3:.2f} ms/call, {reps * dt:.1f} s total")
+    return dict(value=round(value, 4), unit=unit, cores=threads, kind="port", sample=sample,
+                us_per_call=round(dt * 1e6, 1))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default=DEFAULT, choices=sorted(CONFIGS))
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this path runs on a single MI355X); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import qmm as Q
+
+    cfg = CONFIGS[args.config]
+    mode, M, N, K = cfg["mode"], cfg["M"], cfg["N"], cfg["K"]
+    alg = algorithmic(cfg)
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    copies = max(1, math.ceil(ROTATE_BYTES / (alg["w"] + alg["s"])))
+    stream = Q.Stream.torch_current()
+
+    weights = []
+    for r in range(copies):
+        gen.manual_seed(1000 + r)
+        W = (torch.randn((N, K), generator=gen, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+        wq, sc = Q.quantize(Q.Array.from_torch(W), mode, stream=stream)
+        weights.append((wq, sc))
+        del W
+    gen.manual_seed(7)
+    xt = (torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32) * cfg["xscale"]).to(torch.bfloat16)
+    x = Q.Array.from_torch(xt)
+    yt = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    y = Q.Array.from_torch(yt)
+    torch.cuda.synchronize()
+    print(f"[bench] {args.config}: {cfg['workload']}; {copies} weight copies, steps={args.steps} "
+          f"warmup={args.warmup}", file=sys.stderr, flush=True)
+
+    def step(i, st):
+        wq, sc = weights[i % copies]
+        Q.quantized_matmul(x, wq, sc, mode, out=y, stream=st)
+
+    for i in range(args.warmup):
+        step(i, stream)
+    torch.cuda.synchronize()
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if args.no_graph:
+        torch.cuda.synchronize()
+        start.record()
+        for i in range(args.steps):
+            step(i, stream)
+        end.record()
+        end.synchronize()
+    else:
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            cst = Q.Stream.torch_current()
+            step(0, cst)  # one eager call on the capture stream before capture
+            torch.cuda.current_stream().synchronize()
+            with torch.cuda.graph(g, stream=cap):
+                for i in range(args.steps):
+                    step(i, Q.Stream.torch_current())
+        torch.cuda.synchronize()
+        g.replay()  # warm replay
+        torch.cuda.synchronize()
+        start.record()
+        g.replay()
+        end.record()
+        end.synchronize()
+    ms_total = start.elapsed_time(end)
+    ms = ms_total / args.steps
+    sec = ms / 1e3
+    roof = roofline_of(cfg, alg, sec)
+    roof["traffic"] = traffic_from_profiles(args.config)
+
+    cpu = None
+    if not args.no_cpu:
+        wq0, sc0 = weights[0]
+        cpu = cpu_baseline(cfg, xt.view(torch.int16).cpu().numpy().view(np.uint16), wq0.numpy(), sc0.numpy())
+
+    metric = "qmatmul GB/s & % HBM peak at M=1 (nvfp4/mxfp8); TFLOPS & % MFMA at M=4096"
+    unit, value = roof["unit"], roof["achieved"]
+    line = {
+        "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "us_per_call": round(ms * 1e3, 2), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": f"{mode} weights x bf16 (fp32 accumulate)",
+        "data": "synthetic (seeded N(0,1) x, N(0,0.02) W quantized on device)",
+        "config": {"workload": cfg["workload"], "mode": mode, "M": M, "N": N, "K": K, "weight_copies": copies,
+                   "algorithmic_bytes": alg["bytes"], "algorithmic_flops": alg["flops"],
+                   "timing": "eager" if args.no_graph else "hip graph replay"},
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

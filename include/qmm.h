@@ -1,0 +1,191 @@
+/*
+ * qmm.h -- C ABI of the MI355X (gfx950) quantized linear layer.
+ *
+ * Drop-in replacement for the mlx-c entry points that mlx-runner's quantized
+ * linear path binds (reference paths relative to the mlx-runner checkout):
+ *
+ *   mlx_quantized_matmul   src/mlx.zig:265   -> qmm_quantized_matmul
+ *   mlx_dequantize         src/mlx.zig:274   -> qmm_dequantize
+ *   mlx_quantize           src/mlx.zig:278   -> qmm_quantize
+ *   mlx_array / mlx_stream src/mlx.zig:10-11 -> qmm_array / qmm_stream
+ *   mlx_optional_int       src/mlx.zig:41-51 -> qmm_optional_int
+ *   mlx_dtype numbering    src/mlx.zig:21-36 -> qmm_dtype
+ *   error latch            src/mlx.zig:719-868 -> qmm_set_error_handler, qmm_check_error, ...
+ *   check + fault counter  src/mlx.zig:545-595 -> qmm_fault_arm, qmm_op_count
+ *   WeightMap / QuantSpec  src/weights.zig:37-352 -> qmm_weights_* , qmm_infer_quant_spec_json
+ *   namedLinearQ / qlinear src/model.zig:213-260 -> qmm_named_linear_q
+ *
+ * Conventions (same as mlx-c): every op returns 0 on success and non-zero on
+ * failure; a failure also latches its message (first error wins) for the
+ * next qmm_check_error().  Results are returned through an out-handle the
+ * caller owns and frees with qmm_array_free; inputs are borrowed.  Ops are
+ * eager and stream-ordered: a result is valid once its stream is synchronized,
+ * and inputs must stay alive until then.
+ *
+ * All device memory is HBM on the current HIP device.  No torch types appear
+ * in this interface.
+ */
+#ifndef QMM_H
+#define QMM_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- handles (opaque, one pointer wide, as mlx_array / mlx_stream) ---- */
+typedef struct qmm_array_ { void *ctx; } qmm_array;
+typedef struct qmm_stream_ { void *ctx; } qmm_stream;
+typedef struct qmm_vector_array_ { void *ctx; } qmm_vector_array;
+typedef struct qmm_weight_map_ { void *ctx; } qmm_weight_map;
+
+/* dtype codes follow mlx_dtype (src/mlx.zig:21-36). */
+typedef enum {
+  QMM_BOOL = 0, QMM_UINT8 = 1, QMM_UINT16 = 2, QMM_UINT32 = 3, QMM_UINT64 = 4,
+  QMM_INT8 = 5, QMM_INT16 = 6, QMM_INT32 = 7, QMM_INT64 = 8,
+  QMM_FLOAT16 = 9, QMM_FLOAT32 = 10, QMM_FLOAT64 = 11, QMM_BFLOAT16 = 12, QMM_COMPLEX64 = 13
+} qmm_dtype;
+
+typedef struct { int value; bool has_value; } qmm_optional_int;         /* src/mlx.zig:41-51 */
+typedef struct { qmm_dtype value; bool has_value; } qmm_optional_dtype; /* mlx_optional_dtype */
+
+/* ---- arrays ---- */
+/* Empty handle (mlx_array_new). */
+qmm_array qmm_array_new(void);
+/* New HBM array holding a copy of host `data` (mlx_array_new_data).  NULL ctx on failure. */
+qmm_array qmm_array_new_data(const void *data, const int *shape, int dim, qmm_dtype dtype);
+/* Wrap an existing device buffer without copying or taking ownership.  No
+ * mlx-c counterpart: lets a caller hand HBM it already owns (e.g. a loader's
+ * buffer) to the ops.  The buffer must outlive the handle. */
+qmm_array qmm_array_new_device(void *device_ptr, const int *shape, int dim, qmm_dtype dtype);
+int qmm_array_free(qmm_array a);                                  /* mlx_array_free */
+size_t qmm_array_ndim(qmm_array a);                               /* mlx_array_ndim */
+const int *qmm_array_shape(qmm_array a);                          /* mlx_array_shape */
+qmm_dtype qmm_array_dtype(qmm_array a);                           /* mlx_array_dtype */
+size_t qmm_array_size(qmm_array a);                               /* mlx_array_size */
+size_t qmm_array_nbytes(qmm_array a);                             /* mlx_array_nbytes */
+void *qmm_array_data_device(qmm_array a);                         /* device pointer */
+/* Copy the array to host memory after its stream's pending work (the
+ * eval + mlx_array_data_* step).  Returns non-zero on size mismatch. */
+int qmm_array_to_host(void *dst, size_t nbytes, qmm_array a, qmm_stream s);
+
+/* ---- streams ---- */
+qmm_stream qmm_default_gpu_stream_new(void);      /* gpuStream, src/mlx.zig:425-427 (null HIP stream) */
+qmm_stream qmm_stream_new_from_hip(void *hip_stream); /* wrap a caller's hipStream_t (borrowed) */
+int qmm_stream_free(qmm_stream s);
+int qmm_synchronize(qmm_stream s);                /* mlx_synchronize */
+
+/* ---- ops ---- */
+/* y = x @ deq(w).T  (src/mlx.zig:265; called by qlinear, src/model.zig:244-260).
+ *  x: bf16 or f32 [..., M, K]; w: uint32 [N, K*bits/32]; scales: uint8 [N, K/group];
+ *  biases must be the null handle; transpose_w must be true;
+ *  group_size / bits: optional, default by mode (mxfp8 -> 32/8, nvfp4 -> 16/4), else must match;
+ *  mode: "mxfp8" | "nvfp4".  y: [..., M, N] in x's dtype (fp32 accumulation, RNE).
+ * If *res already holds an array of exactly the output shape and dtype its
+ * buffer is written in place (no allocation); otherwise *res is replaced by a
+ * new array. */
+int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array scales, qmm_array biases,
+                         bool transpose_w, qmm_optional_int group_size, qmm_optional_int bits,
+                         const char *mode, qmm_stream s);
+
+/* deq(w) as [N, K] of `dtype` (default bfloat16; float32 and bfloat16 supported)
+ * (src/mlx.zig:274).  biases and global_scale must be null handles. */
+int qmm_dequantize(qmm_array *res, qmm_array w, qmm_array scales, qmm_array biases,
+                   qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
+                   qmm_array global_scale, qmm_optional_dtype dtype, qmm_stream s);
+
+/* [packed uint32, scales uint8] from a bf16/f32 [N, K] matrix (src/mlx.zig:278).
+ * Rounding: mxfp8 shared exponent floor(log2(amax)) - 8, elements RNE to E4M3
+ * saturating at 448; nvfp4 scale RNE_E4M3(amax/6), elements RNE to E2M1,
+ * saturating at 6.  global_scale must be the null handle. */
+int qmm_quantize(qmm_vector_array *res, qmm_array w, qmm_optional_int group_size, qmm_optional_int bits,
+                 const char *mode, qmm_array global_scale, qmm_stream s);
+
+qmm_vector_array qmm_vector_array_new(void);
+int qmm_vector_array_free(qmm_vector_array v);
+size_t qmm_vector_array_size(qmm_vector_array v);
+int qmm_vector_array_get(qmm_array *res, qmm_vector_array v, size_t idx); /* new handle, caller frees */
+
+/* ---- errors (src/mlx.zig:719-868) ---- */
+typedef void (*qmm_error_handler_func)(const char *msg, void *data);
+/* Install a handler called with every error message (after it is latched). */
+int qmm_set_error_handler(qmm_error_handler_func handler, void *data, void (*dtor)(void *));
+bool qmm_error_pending(void);
+/* Memory-class message? (hipErrorOutOfMemory and allocation failures) */
+bool qmm_error_is_memory(const char *msg);
+/* Name of the class the next check would raise ("OutOfMemory" / "MlxFailure"), or NULL; does not consume. */
+const char *qmm_peek_error_name(void);
+/* Consume the latched message into buf; returns its length, or -1 if none. */
+int qmm_take_error(char *buf, size_t len);
+/* Checkpoints: 0 = no error, QMM_ERR_OOM, QMM_ERR_FAILURE; consume the latch.
+ * Env QMM_FAULT_CHUNK=<n> / QMM_FAULT_STEP=<n> latch a synthetic memory error at
+ * the n-th call of qmm_check_error / qmm_check_error_decode (then disarm). */
+#define QMM_ERR_OOM 1
+#define QMM_ERR_FAILURE 2
+int qmm_check_error(void);
+int qmm_check_error_decode(void);
+void qmm_latch_error_for_test(const char *msg);
+void qmm_reset_faults_for_test(void);
+/* Test fault injection at the op chokepoint (src/mlx.zig:562-595): the k-th
+ * subsequent op that would succeed reports failure instead (its outputs stay
+ * valid and freeable).  arm(0) disarms. */
+void qmm_fault_arm(uint64_t k);
+bool qmm_fault_did_fire(void);
+uint64_t qmm_op_count(void);
+
+/* ---- weights (src/weights.zig) ---- */
+typedef enum { QMM_QUANT_NONE = 0, QMM_QUANT_MXFP8 = 1, QMM_QUANT_NVFP4 = 2 } qmm_quant_mode;
+typedef struct { qmm_quant_mode mode; uint32_t group_size; uint32_t bits; } qmm_quant_spec;
+
+/* Error codes of the loader / header checks (WeightsError, src/weights.zig:23-33). */
+#define QMM_WE_BAD_INDEX_JSON 101
+#define QMM_WE_BAD_HEADER 102
+#define QMM_WE_UNSUPPORTED_DTYPE 103
+#define QMM_WE_UNSUPPORTED_LAYOUT 104
+#define QMM_WE_MISSING_TENSOR 105
+#define QMM_WE_DUPLICATE_TENSOR 106
+#define QMM_WE_NONSTANDARD_QUANT 107
+#define QMM_WE_INCONSISTENT_QUANT 108
+#define QMM_WE_AFFINE_UNSUPPORTED 109
+#define QMM_WE_IO 110
+#define QMM_WE_MISSING_WEIGHT 111
+
+/* Parse + validate one safetensors header JSON (parseHeaderJson, src/weights.zig:70-121)
+ * and infer the quant spec from it alone (inferQuantSpec, :130-185).  Host-only.
+ * Returns 0 or a QMM_WE_* code; *n_tensors receives the tensor count. */
+int qmm_infer_quant_spec_json(const char *json, size_t len, qmm_quant_spec *spec, size_t *n_tensors);
+/* Header parse only. */
+int qmm_parse_header_json(const char *json, size_t len, size_t *n_tensors);
+/* Name remap (sanitizeName, :186-202): writes the kept name into out (NUL
+ * terminated); returns 1 kept, 0 dropped, <0 if out is too small. */
+int qmm_sanitize_name(const char *name, char *out, size_t out_len);
+
+/* Load a sharded safetensors checkpoint (model.safetensors.index.json + shards)
+ * into HBM, tensors copied raw from their data_offsets (WeightMap.load, :257-352). */
+int qmm_weights_load(qmm_weight_map *res, const char *model_dir, qmm_stream s);
+int qmm_weights_free(qmm_weight_map m);
+/* Borrowed handle (do not free), or a NULL ctx when absent (WeightMap.get). */
+qmm_array qmm_weights_get(qmm_weight_map m, const char *name);
+size_t qmm_weights_count(qmm_weight_map m);
+qmm_quant_spec qmm_weights_quant(qmm_weight_map m);
+
+/* y = x @ W.T with the checkpoint's quantization honored (namedLinearQ,
+ * src/model.zig:213-233): packed U32 + `<prefix>.scales` -> qmm_quantized_matmul
+ * with the map's group/bits/mode; no scales and non-U32 weight -> dense bf16
+ * linear (src/model.zig:200-211); U32 weight without scales or a name not ending
+ * in ".weight" -> QMM_WE_MISSING_WEIGHT. */
+int qmm_named_linear_q(qmm_array *res, qmm_weight_map m, qmm_array x, const char *name, qmm_stream s);
+/* Dense y = x @ w.T for bf16 x [..., M, K] and bf16 w [N, K] (linear, src/model.zig:200-211). */
+int qmm_linear(qmm_array *res, qmm_array x, qmm_array w, qmm_stream s);
+
+/* Library / device info. */
+const char *qmm_version(void);
+int qmm_device_info(char *buf, size_t len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QMM_H */

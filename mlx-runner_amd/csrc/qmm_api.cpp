@@ -1,0 +1,588 @@
+// C ABI core: arrays, streams, error latch, op chokepoint, and the three ops
+// mlx-runner's quantized linear path binds (src/mlx.zig:265, :274, :278).
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/qmm.h"
+#include "qmm_internal.h"
+#include "qmm_launch.h"
+
+namespace qmm {
+
+// ---------------------------------------------------------------- error latch (src/mlx.zig:719-868)
+namespace {
+std::mutex g_err_mtx;
+std::atomic<bool> g_latched{false};
+char g_err_buf[512];
+size_t g_err_len = 0;
+qmm_error_handler_func g_handler = nullptr;
+void *g_handler_data = nullptr;
+void (*g_handler_dtor)(void *) = nullptr;
+
+// test fault counter at the op chokepoint (src/mlx.zig:562-595)
+std::atomic<uint64_t> g_op_count{0};
+uint64_t g_fault_remaining = 0;
+bool g_fault_fired = false;
+
+// env-armed checkpoint faults (MLX_SERVE_MLX_FAULT_CHUNK / _STEP analogues, src/mlx.zig:807-868)
+struct FaultSite {
+  const char *env;
+  const char *msg;
+  long long at = -1;  // -1: env not read yet
+  unsigned long long seen = 0;
+  long long target() {
+    if (at >= 0) return at;
+    at = 0;
+    if (const char *p = std::getenv(env)) at = std::atoll(p) > 0 ? std::atoll(p) : 0;
+    if (at > 0) std::fprintf(stderr, "[qmm] FAULT INJECTION armed: %s=#%lld\n", env, at);
+    return at;
+  }
+  void maybe_fire() {
+    long long t = target();
+    if (t == 0) return;
+    seen += 1;
+    if ((long long)seen != t) return;
+    at = 0;
+    latch_error(msg);
+  }
+  void reset() {
+    at = -1;
+    seen = 0;
+  }
+};
+FaultSite g_fault_chunk{"QMM_FAULT_CHUNK",
+                        "[qmm] hipErrorOutOfMemory: out of memory (injected by QMM_FAULT_CHUNK)"};
+FaultSite g_fault_step{"QMM_FAULT_STEP", "[qmm] hipErrorOutOfMemory: out of memory (injected by QMM_FAULT_STEP)"};
+}  // namespace
+
+void latch_error(const char *msg) {
+  {
+    std::lock_guard<std::mutex> lk(g_err_mtx);
+    if (!g_latched.load(std::memory_order_acquire)) {  // first error wins
+      size_t n = std::strlen(msg);
+      if (n > sizeof(g_err_buf) - 1) n = sizeof(g_err_buf) - 1;
+      std::memcpy(g_err_buf, msg, n);
+      g_err_buf[n] = 0;
+      g_err_len = n;
+      g_latched.store(true, std::memory_order_release);
+    }
+  }
+  if (g_handler)
+    g_handler(msg, g_handler_data);
+  else
+    std::fprintf(stderr, "[qmm] %s\n", msg);
+}
+
+int fail(const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  latch_error(buf);
+  return 1;
+}
+
+int fail_hip(hipError_t e, const char *what) {
+  return fail("[%s] %s: %s", what, hipGetErrorName(e), hipGetErrorString(e));
+}
+
+// The chokepoint every op returns through: counts ops and applies the armed test fault.
+int finish(int rc) {
+  g_op_count.fetch_add(1, std::memory_order_relaxed);
+  if (rc != 0) return rc;
+  if (g_fault_remaining != 0) {
+    g_fault_remaining -= 1;
+    if (g_fault_remaining == 0) {
+      g_fault_fired = true;
+      return 1;
+    }
+  }
+  return 0;
+}
+
+// ---------------------------------------------------------------- arrays
+size_t dtype_size(qmm_dtype d) {
+  switch (d) {
+    case QMM_BOOL: case QMM_UINT8: case QMM_INT8: return 1;
+    case QMM_UINT16: case QMM_INT16: case QMM_FLOAT16: case QMM_BFLOAT16: return 2;
+    case QMM_UINT32: case QMM_INT32: case QMM_FLOAT32: return 4;
+    case QMM_UINT64: case QMM_INT64: case QMM_FLOAT64: case QMM_COMPLEX64: return 8;
+  }
+  return 0;
+}
+
+size_t Arr::size() const {
+  size_t n = 1;
+  for (int i = 0; i < ndim; ++i) n *= (size_t)shape[i];
+  return n;
+}
+
+namespace {
+bool g_pool_ready = false;
+std::mutex g_pool_mtx;
+void pool_init() {
+  std::lock_guard<std::mutex> lk(g_pool_mtx);
+  if (g_pool_ready) return;
+  g_pool_ready = true;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  hipMemPool_t pool;
+  if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+    uint64_t thr = UINT64_MAX;  // keep freed blocks cached for reuse
+    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &thr);
+  }
+}
+}  // namespace
+
+// Stream-ordered HBM allocation (cached by the device's default pool).
+int alloc_device(void **p, size_t bytes, hipStream_t st) {
+  pool_init();
+  *p = nullptr;
+  if (bytes == 0) bytes = 1;
+  hipError_t e = hipMallocAsync(p, bytes, st);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail("[qmm::malloc] Unable to allocate %zu bytes: %s (out of memory)", bytes, hipGetErrorName(e));
+  }
+  return 0;
+}
+
+Arr *new_arr(const int *shape, int dim, qmm_dtype dtype) {
+  if (dim < 0 || dim > QMM_MAX_DIM) return nullptr;
+  Arr *a = new Arr();
+  a->ndim = dim;
+  for (int i = 0; i < dim; ++i) a->shape[i] = shape[i];
+  a->dtype = dtype;
+  return a;
+}
+
+int alloc_arr(qmm_array *res, const std::vector<int> &shape, qmm_dtype dtype, hipStream_t st, Arr **out) {
+  // Reuse the caller's array when it already has exactly this shape and dtype.
+  Arr *cur = res ? (Arr *)res->ctx : nullptr;
+  if (cur && cur->data && cur->dtype == dtype && cur->ndim == (int)shape.size()) {
+    bool same = true;
+    for (int i = 0; i < cur->ndim; ++i) same &= cur->shape[i] == shape[i];
+    if (same) {
+      *out = cur;
+      return 0;
+    }
+  }
+  Arr *a = new_arr(shape.data(), (int)shape.size(), dtype);
+  if (!a) return fail("[qmm] array rank %zu exceeds %d", shape.size(), QMM_MAX_DIM);
+  if (alloc_device(&a->data, a->nbytes(), st)) {
+    delete a;
+    return 1;
+  }
+  a->owned = true;
+  a->alloc_stream = st;
+  if (cur) release_arr(cur);
+  res->ctx = a;
+  *out = a;
+  return 0;
+}
+
+void release_arr(Arr *a) {
+  if (!a) return;
+  if (a->owned && a->data) (void)hipFreeAsync(a->data, a->alloc_stream);
+  delete a;
+}
+
+hipStream_t stream_of(qmm_stream s) { return s.ctx ? ((Stream *)s.ctx)->h : (hipStream_t)0; }
+
+}  // namespace qmm
+
+using namespace qmm;
+
+// ================================================================ C ABI
+
+extern "C" {
+
+const char *qmm_version(void) { return "qmm-gfx950 0.1"; }
+
+int qmm_device_info(char *buf, size_t len) {
+  int dev = 0;
+  hipDeviceProp_t p;
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail("[qmm_device_info] no HIP device");
+  }
+  std::snprintf(buf, len, "%s %s CUs=%d clock_khz=%d mem_clock_khz=%d bus_bits=%d hbm_bytes=%zu l2=%d",
+                p.name, p.gcnArchName, p.multiProcessorCount, p.clockRate, p.memoryClockRate, p.memoryBusWidth,
+                (size_t)p.totalGlobalMem, p.l2CacheSize);
+  return 0;
+}
+
+// ---------------- arrays
+qmm_array qmm_array_new(void) { return qmm_array{nullptr}; }
+
+qmm_array qmm_array_new_data(const void *data, const int *shape, int dim, qmm_dtype dtype) {
+  Arr *a = new_arr(shape, dim, dtype);
+  if (!a || dtype_size(dtype) == 0) {
+    delete a;
+    fail("[qmm_array_new_data] bad rank or dtype");
+    return qmm_array{nullptr};
+  }
+  if (alloc_device(&a->data, a->nbytes(), (hipStream_t)0)) {
+    delete a;
+    return qmm_array{nullptr};
+  }
+  a->owned = true;
+  a->alloc_stream = (hipStream_t)0;
+  if (a->nbytes()) {
+    hipError_t e = hipMemcpy(a->data, data, a->nbytes(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      fail_hip(e, "qmm_array_new_data");
+      release_arr(a);
+      return qmm_array{nullptr};
+    }
+  }
+  return qmm_array{a};
+}
+
+qmm_array qmm_array_new_device(void *device_ptr, const int *shape, int dim, qmm_dtype dtype) {
+  Arr *a = new_arr(shape, dim, dtype);
+  if (!a || dtype_size(dtype) == 0) {
+    delete a;
+    fail("[qmm_array_new_device] bad rank or dtype");
+    return qmm_array{nullptr};
+  }
+  for (int i = 0; i < dim; ++i)
+    if (shape[i] < 0) {
+      delete a;
+      fail("[qmm_array_new_device] negative dimension");
+      return qmm_array{nullptr};
+    }
+  a->data = device_ptr;
+  a->owned = false;
+  return qmm_array{a};
+}
+
+int qmm_array_free(qmm_array a) {
+  release_arr((Arr *)a.ctx);
+  return 0;
+}
+size_t qmm_array_ndim(qmm_array a) { return a.ctx ? ((Arr *)a.ctx)->ndim : 0; }
+const int *qmm_array_shape(qmm_array a) { return a.ctx ? ((Arr *)a.ctx)->shape : nullptr; }
+qmm_dtype qmm_array_dtype(qmm_array a) { return a.ctx ? ((Arr *)a.ctx)->dtype : QMM_BOOL; }
+size_t qmm_array_size(qmm_array a) { return a.ctx ? ((Arr *)a.ctx)->size() : 0; }
+size_t qmm_array_nbytes(qmm_array a) { return a.ctx ? ((Arr *)a.ctx)->nbytes() : 0; }
+void *qmm_array_data_device(qmm_array a) { return a.ctx ? ((Arr *)a.ctx)->data : nullptr; }
+
+int qmm_array_to_host(void *dst, size_t nbytes, qmm_array a, qmm_stream s) {
+  Arr *x = (Arr *)a.ctx;
+  if (!x) return finish(fail("[qmm_array_to_host] empty array"));
+  if (nbytes != x->nbytes()) return finish(fail("[qmm_array_to_host] size %zu != array bytes %zu", nbytes, x->nbytes()));
+  hipStream_t st = stream_of(s);
+  hipError_t e = hipMemcpyAsync(dst, x->data, nbytes, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return finish(fail_hip(e, "qmm_array_to_host"));
+  return finish(0);
+}
+
+// ---------------- streams
+qmm_stream qmm_default_gpu_stream_new(void) {
+  Stream *s = new Stream();
+  s->h = (hipStream_t)0;
+  return qmm_stream{s};
+}
+qmm_stream qmm_stream_new_from_hip(void *hip_stream) {
+  Stream *s = new Stream();
+  s->h = (hipStream_t)hip_stream;
+  return qmm_stream{s};
+}
+int qmm_stream_free(qmm_stream s) {
+  delete (Stream *)s.ctx;
+  return 0;
+}
+int qmm_synchronize(qmm_stream s) {
+  hipError_t e = hipStreamSynchronize(stream_of(s));
+  if (e != hipSuccess) return finish(fail_hip(e, "qmm_synchronize"));
+  return finish(0);
+}
+
+// ---------------- errors
+int qmm_set_error_handler(qmm_error_handler_func handler, void *data, void (*dtor)(void *)) {
+  std::lock_guard<std::mutex> lk(g_err_mtx);
+  if (g_handler_dtor && g_handler_data) g_handler_dtor(g_handler_data);
+  g_handler = handler;
+  g_handler_data = data;
+  g_handler_dtor = dtor;
+  return 0;
+}
+
+bool qmm_error_pending(void) { return g_latched.load(std::memory_order_acquire); }
+
+bool qmm_error_is_memory(const char *msg) {
+  static const char *needles[] = {"Insufficient Memory", "insufficient memory", "Unable to allocate",
+                                  "Resource limit",      "out of memory",       "Out of memory",
+                                  "maximum allowed buffer size", "hipErrorOutOfMemory"};
+  for (const char *n : needles)
+    if (std::strstr(msg, n)) return true;
+  return false;
+}
+
+const char *qmm_peek_error_name(void) {
+  if (!g_latched.load(std::memory_order_acquire)) return nullptr;
+  std::lock_guard<std::mutex> lk(g_err_mtx);
+  return qmm_error_is_memory(g_err_buf) ? "OutOfMemory" : "MlxFailure";
+}
+
+int qmm_take_error(char *buf, size_t len) {
+  if (!g_latched.load(std::memory_order_acquire)) return -1;
+  std::lock_guard<std::mutex> lk(g_err_mtx);
+  size_t n = g_err_len;
+  if (buf && len) {
+    size_t c = n < len - 1 ? n : len - 1;
+    std::memcpy(buf, g_err_buf, c);
+    buf[c] = 0;
+  }
+  g_err_len = 0;
+  g_err_buf[0] = 0;
+  g_latched.store(false, std::memory_order_release);
+  return (int)n;
+}
+
+static int consume_latch() {
+  if (!g_latched.load(std::memory_order_acquire)) return 0;
+  char buf[512];
+  if (qmm_take_error(buf, sizeof buf) < 0) return 0;
+  return qmm_error_is_memory(buf) ? QMM_ERR_OOM : QMM_ERR_FAILURE;
+}
+
+int qmm_check_error(void) {
+  g_fault_chunk.maybe_fire();
+  return consume_latch();
+}
+int qmm_check_error_decode(void) {
+  g_fault_step.maybe_fire();
+  return consume_latch();
+}
+void qmm_latch_error_for_test(const char *msg) { latch_error(msg); }
+void qmm_reset_faults_for_test(void) {
+  g_fault_chunk.reset();
+  g_fault_step.reset();
+  qmm_take_error(nullptr, 0);
+}
+void qmm_fault_arm(uint64_t k) {
+  g_fault_remaining = k;
+  g_fault_fired = false;
+}
+bool qmm_fault_did_fire(void) { return g_fault_fired; }
+uint64_t qmm_op_count(void) { return g_op_count.load(std::memory_order_relaxed); }
+
+// ---------------- vector_array
+qmm_vector_array qmm_vector_array_new(void) { return qmm_vector_array{new VecArr()}; }
+int qmm_vector_array_free(qmm_vector_array v) {
+  VecArr *p = (VecArr *)v.ctx;
+  if (!p) return 0;
+  for (Arr *a : p->items) release_arr(a);
+  delete p;
+  return 0;
+}
+size_t qmm_vector_array_size(qmm_vector_array v) { return v.ctx ? ((VecArr *)v.ctx)->items.size() : 0; }
+int qmm_vector_array_get(qmm_array *res, qmm_vector_array v, size_t idx) {
+  VecArr *p = (VecArr *)v.ctx;
+  if (!p || idx >= p->items.size()) return finish(fail("[qmm_vector_array_get] index %zu out of range", idx));
+  // A new borrowed view of the vector's array (the vector keeps ownership, as
+  // mlx arrays share their buffer); free the view with qmm_array_free.
+  Arr *src = p->items[idx];
+  Arr *a = new_arr(src->shape, src->ndim, src->dtype);
+  a->data = src->data;
+  a->owned = false;
+  if (res->ctx) release_arr((Arr *)res->ctx);
+  res->ctx = a;
+  return finish(0);
+}
+
+// ---------------- ops
+static int parse_mode(const char *mode, qmm_optional_int gs, qmm_optional_int bits, const char *op, int *m_out) {
+  if (!mode) return fail("[%s] mode is null", op);
+  int m;
+  if (std::strcmp(mode, "mxfp8") == 0)
+    m = MXFP8;
+  else if (std::strcmp(mode, "nvfp4") == 0)
+    m = NVFP4;
+  else
+    return fail("[%s] Unsupported quantization mode '%s' (this library serves mxfp8 and nvfp4)", op, mode);
+  const int g = m == MXFP8 ? 32 : 16, b = m == MXFP8 ? 8 : 4;
+  if (gs.has_value && gs.value != g) return fail("[%s] %s requires group_size %d, got %d", op, mode, g, gs.value);
+  if (bits.has_value && bits.value != b) return fail("[%s] %s requires bits %d, got %d", op, mode, b, bits.value);
+  *m_out = m;
+  return 0;
+}
+
+// Validate packed weights + scales, derive N and K.
+static int check_wq(const Arr *w, const Arr *sc, int mode, const char *op, int *N, int *K) {
+  const int g = mode == MXFP8 ? 32 : 16, bits = mode == MXFP8 ? 8 : 4;
+  if (!w || !sc) return fail("[%s] missing weight or scales", op);
+  if (w->dtype != QMM_UINT32 || w->ndim != 2)
+    return fail("[%s] packed weight must be a 2D uint32 array", op);
+  if (sc->dtype != QMM_UINT8 || sc->ndim != 2) return fail("[%s] scales must be a 2D uint8 array", op);
+  *N = w->shape[0];
+  *K = (int)((int64_t)w->shape[1] * 32 / bits);
+  if (sc->shape[0] != *N || (int64_t)sc->shape[1] * g != *K)
+    return fail("[%s] scales shape [%d, %d] does not match weight [%d, %d] for group %d", op, sc->shape[0],
+                sc->shape[1], w->shape[0], w->shape[1], g);
+  return 0;
+}
+
+int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array scales, qmm_array biases,
+                         bool transpose_w, qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
+                         qmm_stream s) {
+  const char *op = "quantized_matmul";
+  if (!res) return finish(fail("[%s] null result pointer", op));
+  int m;
+  if (parse_mode(mode, group_size, bits, op, &m)) return finish(1);
+  if (biases.ctx) return finish(fail("[%s] %s takes no biases", op, mode));
+  if (!transpose_w) return finish(fail("[%s] only transpose_w = true is supported", op));
+  Arr *xa = (Arr *)x.ctx, *wa = (Arr *)w.ctx, *sa = (Arr *)scales.ctx;
+  if (!xa) return finish(fail("[%s] missing x", op));
+  int N, K;
+  if (check_wq(wa, sa, m, op, &N, &K)) return finish(1);
+  if (xa->dtype != QMM_BFLOAT16 && xa->dtype != QMM_FLOAT32)
+    return finish(fail("[%s] x must be bfloat16 or float32", op));
+  if (xa->ndim < 1) return finish(fail("[%s] x must have at least one dimension", op));
+  if (xa->shape[xa->ndim - 1] != K)
+    return finish(fail("[%s] Last dimension of x (%d) does not match the weight's K (%d)", op,
+                       xa->shape[xa->ndim - 1], K));
+  int64_t M = 1;
+  for (int i = 0; i < xa->ndim - 1; ++i) M *= xa->shape[i];
+  if (M > INT32_MAX) return finish(fail("[%s] too many rows", op));
+  std::vector<int> oshape(xa->shape, xa->shape + xa->ndim);
+  oshape.back() = N;
+  hipStream_t st = stream_of(s);
+  Arr *ya;
+  if (alloc_arr(res, oshape, xa->dtype, st, &ya)) return finish(1);
+  if (M == 0 || N == 0) return finish(0);
+
+  QmmArgs a;
+  a.mode = m;
+  a.x_f32 = xa->dtype == QMM_FLOAT32;
+  a.M = (int)M;
+  a.N = N;
+  a.K = K;
+  a.x = xa->data;
+  a.w = (const uint8_t *)wa->data;
+  a.s = (const uint8_t *)sa->data;
+  a.y = ya->data;
+  const bool aligned = (((uintptr_t)a.x | (uintptr_t)a.w) & 15) == 0;
+  hipError_t e = hipSuccess;
+  if (K == 0) {
+    e = launch_fill_zero(a.y, ya->nbytes(), st);
+  } else if (a.M <= QMV_MAX_M) {
+    e = (aligned && qmv_fast_ok(a)) ? launch_qmv(a, st) : launch_qmv_generic(a, st);
+  } else if (aligned && gemm_ok(a)) {
+    e = launch_gemm(a, st);
+  } else {
+    // f32 x (or an unaligned view) with many rows: decode kernel over row blocks of 8.
+    const size_t esz = a.x_f32 ? 4 : 2;
+    for (int m0 = 0; m0 < a.M && e == hipSuccess; m0 += QMV_MAX_M) {
+      QmmArgs b = a;
+      b.M = a.M - m0 < QMV_MAX_M ? a.M - m0 : QMV_MAX_M;
+      b.x = (const char *)a.x + (size_t)m0 * K * esz;
+      b.y = (char *)a.y + (size_t)m0 * N * esz;
+      const bool al = (((uintptr_t)b.x | (uintptr_t)b.w) & 15) == 0;
+      e = (al && qmv_fast_ok(b)) ? launch_qmv(b, st) : launch_qmv_generic(b, st);
+    }
+  }
+  if (e != hipSuccess) return finish(fail_hip(e, op));
+  return finish(0);
+}
+
+int qmm_dequantize(qmm_array *res, qmm_array w, qmm_array scales, qmm_array biases, qmm_optional_int group_size,
+                   qmm_optional_int bits, const char *mode, qmm_array global_scale, qmm_optional_dtype dtype,
+                   qmm_stream s) {
+  const char *op = "dequantize";
+  if (!res) return finish(fail("[%s] null result pointer", op));
+  int m;
+  if (parse_mode(mode, group_size, bits, op, &m)) return finish(1);
+  if (biases.ctx) return finish(fail("[%s] %s takes no biases", op, mode));
+  if (global_scale.ctx) return finish(fail("[%s] global_scale is not supported", op));
+  qmm_dtype dt = dtype.has_value ? dtype.value : QMM_BFLOAT16;
+  if (dt != QMM_BFLOAT16 && dt != QMM_FLOAT32) return finish(fail("[%s] dtype must be bfloat16 or float32", op));
+  Arr *wa = (Arr *)w.ctx, *sa = (Arr *)scales.ctx;
+  int N, K;
+  if (check_wq(wa, sa, m, op, &N, &K)) return finish(1);
+  hipStream_t st = stream_of(s);
+  Arr *o;
+  if (alloc_arr(res, {N, K}, dt, st, &o)) return finish(1);
+  hipError_t e = launch_dequant(m, (const uint8_t *)wa->data, (const uint8_t *)sa->data, N, K, o->data,
+                                dt == QMM_FLOAT32, st);
+  if (e != hipSuccess) return finish(fail_hip(e, op));
+  return finish(0);
+}
+
+int qmm_quantize(qmm_vector_array *res, qmm_array w, qmm_optional_int group_size, qmm_optional_int bits,
+                 const char *mode, qmm_array global_scale, qmm_stream s) {
+  const char *op = "quantize";
+  if (!res) return finish(fail("[%s] null result pointer", op));
+  int m;
+  if (parse_mode(mode, group_size, bits, op, &m)) return finish(1);
+  if (global_scale.ctx) return finish(fail("[%s] global_scale is not supported", op));
+  Arr *wa = (Arr *)w.ctx;
+  if (!wa || wa->ndim != 2 || (wa->dtype != QMM_BFLOAT16 && wa->dtype != QMM_FLOAT32))
+    return finish(fail("[%s] w must be a 2D bfloat16 or float32 array", op));
+  const int g = m == MXFP8 ? 32 : 16, b = m == MXFP8 ? 8 : 4;
+  const int N = wa->shape[0], K = wa->shape[1];
+  if (K % g != 0) return finish(fail("[%s] the last dimension (%d) must be divisible by the group size %d", op, K, g));
+  hipStream_t st = stream_of(s);
+  VecArr *v = new VecArr();
+  Arr *q = new_arr(std::vector<int>{N, K * b / 32}.data(), 2, QMM_UINT32);
+  Arr *sc = new_arr(std::vector<int>{N, K / g}.data(), 2, QMM_UINT8);
+  v->items = {q, sc};
+  for (Arr *a : v->items) {
+    a->owned = true;
+    a->alloc_stream = st;
+    if (alloc_device(&a->data, a->nbytes(), st)) {
+      qmm_vector_array_free(qmm_vector_array{v});
+      return finish(1);
+    }
+  }
+  hipError_t e = launch_quantize(m, wa->data, wa->dtype == QMM_FLOAT32, N, K, (uint32_t *)q->data,
+                                 (uint8_t *)sc->data, st);
+  if (e != hipSuccess) {
+    qmm_vector_array_free(qmm_vector_array{v});
+    return finish(fail_hip(e, op));
+  }
+  if (res->ctx) qmm_vector_array_free(*res);
+  res->ctx = v;
+  return finish(0);
+}
+
+int qmm_linear(qmm_array *res, qmm_array x, qmm_array w, qmm_stream s) {
+  const char *op = "linear";
+  if (!res) return finish(fail("[%s] null result pointer", op));
+  Arr *xa = (Arr *)x.ctx, *wa = (Arr *)w.ctx;
+  if (!xa || !wa) return finish(fail("[%s] missing x or w", op));
+  if (xa->dtype != QMM_BFLOAT16 || wa->dtype != QMM_BFLOAT16 || wa->ndim != 2 || xa->ndim < 1)
+    return finish(fail("[%s] x [..., K] and w [N, K] must be bfloat16", op));
+  const int N = wa->shape[0], K = wa->shape[1];
+  if (xa->shape[xa->ndim - 1] != K)
+    return finish(fail("[matmul] Last dimension of first input (%d) must match the weight (%d)",
+                       xa->shape[xa->ndim - 1], K));
+  if (K % 16 != 0 || (((uintptr_t)xa->data | (uintptr_t)wa->data) & 15) != 0)
+    return finish(fail("[%s] K must be a multiple of 16 and operands 16-byte aligned", op));
+  int64_t M = 1;
+  for (int i = 0; i < xa->ndim - 1; ++i) M *= xa->shape[i];
+  std::vector<int> oshape(xa->shape, xa->shape + xa->ndim);
+  oshape.back() = N;
+  hipStream_t st = stream_of(s);
+  Arr *ya;
+  if (alloc_arr(res, oshape, QMM_BFLOAT16, st, &ya)) return finish(1);
+  if (M == 0 || N == 0) return finish(0);
+  hipError_t e = launch_linear_bf16((const uint16_t *)xa->data, (const uint16_t *)wa->data, (uint16_t *)ya->data,
+                                    (int)M, N, K, st);
+  if (e != hipSuccess) return finish(fail_hip(e, op));
+  return finish(0);
+}
+
+}  // extern "C"

@@ -1,0 +1,44 @@
+// Internal launcher interface between the C ABI (qmm_api.cpp) and the HIP kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qmm {
+
+enum Mode : int { MXFP8 = 0, NVFP4 = 1 };
+
+constexpr int QMV_MAX_M = 8;  // rows of x served by the decode (GEMV / skinny) kernels
+
+struct QmmArgs {
+  int mode;        // 0 = mxfp8, 1 = nvfp4
+  bool x_f32;      // x (and y) float32 instead of bfloat16
+  int M, N, K;     // y[M, N] = x[M, K] @ deq(W[N, K]).T
+  const void *x;
+  const uint8_t *w;  // packed rows, K*bits/8 bytes each
+  const uint8_t *s;  // scale bytes, K/group per row
+  void *y;
+};
+
+bool qmv_fast_ok(const QmmArgs &a);
+hipError_t launch_qmv(const QmmArgs &a, hipStream_t st);
+hipError_t launch_qmv_generic(const QmmArgs &a, hipStream_t st);
+
+// Prefill GEMM (M > QMV_MAX_M).
+bool gemm_ok(const QmmArgs &a);
+hipError_t launch_gemm(const QmmArgs &a, hipStream_t st);
+
+// dequant: out [N, K] float32 (out_f32) or bfloat16.
+hipError_t launch_dequant(int mode, const uint8_t *w, const uint8_t *s, int64_t N, int64_t K, void *out,
+                          bool out_f32, hipStream_t st);
+// quantize: in [N, K] float32 (in_f32) or bfloat16 -> packed words + scale bytes.
+hipError_t launch_quantize(int mode, const void *in, bool in_f32, int64_t N, int64_t K, uint32_t *wq, uint8_t *s,
+                           hipStream_t st);
+
+// Zero-fill `bytes` of device memory.
+hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st);
+
+// Dense bf16 y[M, N] = x[M, K] @ w[N, K].T (fp32 accumulate, RNE).
+hipError_t launch_linear_bf16(const uint16_t *x, const uint16_t *w, uint16_t *y, int M, int N, int K,
+                              hipStream_t st);
+
+}  // namespace qmm

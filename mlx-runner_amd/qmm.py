@@ -1,0 +1,364 @@
+"""ctypes binding of libqmm.so (the C ABI declared in include/qmm.h).
+
+This is the Python-side stub of the boundary: the same calls mlx-runner's Zig
+code makes through `extern "c"` declarations (src/mlx.zig:265, :274, :278),
+used by the tests and the benchmark.  Device memory may come from torch
+(borrowed through `Array.from_torch`); torch is only plumbing here.
+
+Importing this module loads libqmm.so and raises if it is missing: there is no
+fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, byref, c_bool, c_char_p, c_int, c_size_t, c_uint32, c_uint64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libqmm.so"
+HEADER = HERE.parent / "include" / "qmm.h"
+
+if not LIB_PATH.exists():
+    raise ImportError(f"{LIB_PATH} is not built; run `python mlx-runner_amd/build.py` (hipcc, gfx950)")
+
+
+class qmm_array(ctypes.Structure):
+    _fields_ = [("ctx", c_void_p)]
+
+
+class qmm_stream(ctypes.Structure):
+    _fields_ = [("ctx", c_void_p)]
+
+
+class qmm_vector_array(ctypes.Structure):
+    _fields_ = [("ctx", c_void_p)]
+
+
+class qmm_weight_map(ctypes.Structure):
+    _fields_ = [("ctx", c_void_p)]
+
+
+class qmm_optional_int(ctypes.Structure):
+    _fields_ = [("value", c_int), ("has_value", c_bool)]
+
+
+class qmm_optional_dtype(ctypes.Structure):
+    _fields_ = [("value", c_int), ("has_value", c_bool)]
+
+
+class qmm_quant_spec(ctypes.Structure):
+    _fields_ = [("mode", c_int), ("group_size", c_uint32), ("bits", c_uint32)]
+
+
+UINT8, UINT16, UINT32, INT32, FLOAT16, FLOAT32, BFLOAT16 = 1, 2, 3, 7, 9, 10, 12
+ERR_OOM, ERR_FAILURE = 1, 2
+QUANT_NONE, QUANT_MXFP8, QUANT_NVFP4 = 0, 1, 2
+WE = {101: "BadIndexJson", 102: "BadHeader", 103: "UnsupportedDtype", 104: "UnsupportedLayout",
+      105: "MissingTensor", 106: "DuplicateTensor", 107: "NonstandardQuant", 108: "InconsistentQuant",
+      109: "AffineUnsupported", 110: "IO", 111: "MissingWeight"}
+
+lib = ctypes.CDLL(str(LIB_PATH))
+
+ERROR_HANDLER = ctypes.CFUNCTYPE(None, c_char_p, c_void_p)
+_SIGS = {
+    "qmm_version": (c_char_p, []),
+    "qmm_device_info": (c_int, [c_char_p, c_size_t]),
+    "qmm_array_new": (qmm_array, []),
+    "qmm_array_new_data": (qmm_array, [c_void_p, POINTER(c_int), c_int, c_int]),
+    "qmm_array_new_device": (qmm_array, [c_void_p, POINTER(c_int), c_int, c_int]),
+    "qmm_array_free": (c_int, [qmm_array]),
+    "qmm_array_ndim": (c_size_t, [qmm_array]),
+    "qmm_array_shape": (POINTER(c_int), [qmm_array]),
+    "qmm_array_dtype": (c_int, [qmm_array]),
+    "qmm_array_size": (c_size_t, [qmm_array]),
+    "qmm_array_nbytes": (c_size_t, [qmm_array]),
+    "qmm_array_data_device": (c_void_p, [qmm_array]),
+    "qmm_array_to_host": (c_int, [c_void_p, c_size_t, qmm_array, qmm_stream]),
+    "qmm_default_gpu_stream_new": (qmm_stream, []),
+    "qmm_stream_new_from_hip": (qmm_stream, [c_void_p]),
+    "qmm_stream_free": (c_int, [qmm_stream]),
+    "qmm_synchronize": (c_int, [qmm_stream]),
+    "qmm_quantized_matmul": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_array, qmm_array, c_bool,
+                                     qmm_optional_int, qmm_optional_int, c_char_p, qmm_stream]),
+    "qmm_dequantize": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_array, qmm_optional_int,
+                               qmm_optional_int, c_char_p, qmm_array, qmm_optional_dtype, qmm_stream]),
+    "qmm_quantize": (c_int, [POINTER(qmm_vector_array), qmm_array, qmm_optional_int, qmm_optional_int, c_char_p,
+                             qmm_array, qmm_stream]),
+    "qmm_vector_array_new": (qmm_vector_array, []),
+    "qmm_vector_array_free": (c_int, [qmm_vector_array]),
+    "qmm_vector_array_size": (c_size_t, [qmm_vector_array]),
+    "qmm_vector_array_get": (c_int, [POINTER(qmm_array), qmm_vector_array, c_size_t]),
+    "qmm_set_error_handler": (c_int, [ERROR_HANDLER, c_void_p, c_void_p]),
+    "qmm_error_pending": (c_bool, []),
+    "qmm_error_is_memory": (c_bool, [c_char_p]),
+    "qmm_peek_error_name": (c_char_p, []),
+    "qmm_take_error": (c_int, [c_char_p, c_size_t]),
+    "qmm_check_error": (c_int, []),
+    "qmm_check_error_decode": (c_int, []),
+    "qmm_latch_error_for_test": (None, [c_char_p]),
+    "qmm_reset_faults_for_test": (None, []),
+    "qmm_fault_arm": (None, [c_uint64]),
+    "qmm_fault_did_fire": (c_bool, []),
+    "qmm_op_count": (c_uint64, []),
+    "qmm_infer_quant_spec_json": (c_int, [c_char_p, c_size_t, POINTER(qmm_quant_spec), POINTER(c_size_t)]),
+    "qmm_parse_header_json": (c_int, [c_char_p, c_size_t, POINTER(c_size_t)]),
+    "qmm_sanitize_name": (c_int, [c_char_p, c_char_p, c_size_t]),
+    "qmm_weights_load": (c_int, [POINTER(qmm_weight_map), c_char_p, qmm_stream]),
+    "qmm_weights_free": (c_int, [qmm_weight_map]),
+    "qmm_weights_get": (qmm_array, [qmm_weight_map, c_char_p]),
+    "qmm_weights_count": (c_size_t, [qmm_weight_map]),
+    "qmm_weights_quant": (qmm_quant_spec, [qmm_weight_map]),
+    "qmm_named_linear_q": (c_int, [POINTER(qmm_array), qmm_weight_map, qmm_array, c_char_p, qmm_stream]),
+    "qmm_linear": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_stream]),
+}
+for _name, (_res, _args) in _SIGS.items():
+    _f = getattr(lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+
+class QmmError(RuntimeError):
+    """An op returned non-zero; carries the latched message."""
+
+
+def opt_int(v=None) -> qmm_optional_int:
+    return qmm_optional_int(0, False) if v is None else qmm_optional_int(int(v), True)
+
+
+def take_error() -> str | None:
+    buf = ctypes.create_string_buffer(512)
+    n = lib.qmm_take_error(buf, 512)
+    return None if n < 0 else buf.value.decode()
+
+
+def check(rc: int, what: str = "qmm"):
+    """The `check` chokepoint of the reference binding (src/mlx.zig:589-595)."""
+    if rc != 0:
+        msg = take_error()
+        raise QmmError(f"{what} failed (rc={rc}): {msg}")
+
+
+_TORCH_DTYPES = None
+
+
+def _torch_dtype_map():
+    global _TORCH_DTYPES
+    if _TORCH_DTYPES is None:
+        import torch
+
+        _TORCH_DTYPES = {torch.uint8: UINT8, torch.int32: UINT32, torch.bfloat16: BFLOAT16,
+                         torch.float32: FLOAT32, torch.uint32: UINT32}
+    return _TORCH_DTYPES
+
+
+class Stream:
+    def __init__(self, hip_stream: int | None = None):
+        self.h = lib.qmm_default_gpu_stream_new() if hip_stream is None else lib.qmm_stream_new_from_hip(hip_stream)
+
+    @classmethod
+    def torch_current(cls) -> "Stream":
+        import torch
+
+        return cls(torch.cuda.current_stream().cuda_stream)
+
+    def sync(self):
+        check(lib.qmm_synchronize(self.h), "synchronize")
+
+    def __del__(self):
+        try:
+            lib.qmm_stream_free(self.h)
+        except Exception:
+            pass
+
+
+class Array:
+    """Owns a qmm_array handle (freed on deletion)."""
+
+    def __init__(self, h: qmm_array | None = None, keepalive=None):
+        self.h = h if h is not None else lib.qmm_array_new()
+        self._keep = keepalive
+
+    @classmethod
+    def from_torch(cls, t, dtype: int | None = None) -> "Array":
+        """Borrow a contiguous CUDA tensor's HBM (no copy)."""
+        assert t.is_cuda and t.is_contiguous()
+        dt = dtype if dtype is not None else _torch_dtype_map()[t.dtype]
+        shape = (c_int * max(t.dim(), 1))(*t.shape)
+        h = lib.qmm_array_new_device(c_void_p(t.data_ptr()), shape, t.dim(), dt)
+        if not h.ctx:
+            check(1, "array_new_device")
+        return cls(h, keepalive=t)
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray, dtype: int) -> "Array":
+        a = np.ascontiguousarray(a)
+        shape = (c_int * max(a.ndim, 1))(*a.shape)
+        h = lib.qmm_array_new_data(c_void_p(a.ctypes.data), shape, a.ndim, dtype)
+        if not h.ctx:
+            check(1, "array_new_data")
+        return cls(h)
+
+    @property
+    def shape(self):
+        n = lib.qmm_array_ndim(self.h)
+        p = lib.qmm_array_shape(self.h)
+        return tuple(p[i] for i in range(n))
+
+    @property
+    def dtype(self) -> int:
+        return lib.qmm_array_dtype(self.h)
+
+    @property
+    def ptr(self) -> int:
+        return lib.qmm_array_data_device(self.h) or 0
+
+    def numpy(self, stream: Stream | None = None) -> np.ndarray:
+        npdt = {UINT8: np.uint8, UINT32: np.uint32, FLOAT32: np.float32, BFLOAT16: np.uint16}[self.dtype]
+        out = np.empty(self.shape, dtype=npdt)
+        s = stream or Stream()
+        check(lib.qmm_array_to_host(c_void_p(out.ctypes.data), out.nbytes, self.h, s.h), "array_to_host")
+        return out
+
+    def free(self):
+        if self.h is not None and self.h.ctx:
+            lib.qmm_array_free(self.h)
+        self.h = qmm_array(None)
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _stream(stream):
+    return stream if stream is not None else Stream()
+
+
+def quantized_matmul(x: Array, w: Array, scales: Array, mode: str, *, group_size=None, bits=None,
+                     out: Array | None = None, transpose: bool = True, biases: Array | None = None,
+                     stream: Stream | None = None) -> Array:
+    res = out if out is not None else Array()
+    s = _stream(stream)
+    check(lib.qmm_quantized_matmul(byref(res.h), x.h, w.h, scales.h, biases.h if biases else qmm_array(None),
+                                   transpose, opt_int(group_size), opt_int(bits), mode.encode(), s.h),
+          "quantized_matmul")
+    return res
+
+
+def dequantize(w: Array, scales: Array, mode: str, *, dtype: int | None = None, group_size=None, bits=None,
+               stream: Stream | None = None) -> Array:
+    res = Array()
+    s = _stream(stream)
+    od = qmm_optional_dtype(0, False) if dtype is None else qmm_optional_dtype(dtype, True)
+    check(lib.qmm_dequantize(byref(res.h), w.h, scales.h, qmm_array(None), opt_int(group_size), opt_int(bits),
+                             mode.encode(), qmm_array(None), od, s.h), "dequantize")
+    return res
+
+
+class _VectorHolder:
+    """Keeps a qmm_vector_array (and so its buffers) alive while views exist."""
+
+    def __init__(self, v: qmm_vector_array):
+        self.v = v
+
+    def __del__(self):
+        try:
+            lib.qmm_vector_array_free(self.v)
+        except Exception:
+            pass
+
+
+def quantize(w: Array, mode: str, *, group_size=None, bits=None, stream: Stream | None = None):
+    """(packed uint32 [N, K*bits/32], scales uint8 [N, K/group]), both resident in HBM."""
+    v = lib.qmm_vector_array_new()
+    s = _stream(stream)
+    rc = lib.qmm_quantize(byref(v), w.h, opt_int(group_size), opt_int(bits), mode.encode(), qmm_array(None), s.h)
+    holder = _VectorHolder(v)
+    check(rc, "quantize")
+    outs = []
+    for i in range(lib.qmm_vector_array_size(v)):
+        view = Array(keepalive=holder)
+        check(lib.qmm_vector_array_get(byref(view.h), v, i), "vector_array_get")
+        outs.append(view)
+    return outs[0], outs[1]
+
+
+def linear(x: Array, w: Array, *, stream: Stream | None = None) -> Array:
+    res = Array()
+    check(lib.qmm_linear(byref(res.h), x.h, w.h, _stream(stream).h), "linear")
+    return res
+
+
+def infer_quant_spec_json(header: str):
+    b = header.encode()
+    spec = qmm_quant_spec()
+    n = c_size_t(0)
+    rc = lib.qmm_infer_quant_spec_json(b, len(b), byref(spec), byref(n))
+    if rc:
+        return WE.get(rc, rc)
+    return {QUANT_NONE: "none", QUANT_MXFP8: "mxfp8", QUANT_NVFP4: "nvfp4"}[spec.mode], spec.group_size, spec.bits
+
+
+def parse_header_json(header: str):
+    b = header.encode()
+    n = c_size_t(0)
+    rc = lib.qmm_parse_header_json(b, len(b), byref(n))
+    return WE.get(rc, rc) if rc else n.value
+
+
+def sanitize_name(name: str):
+    buf = ctypes.create_string_buffer(4096)
+    rc = lib.qmm_sanitize_name(name.encode(), buf, 4096)
+    return buf.value.decode() if rc == 1 else None
+
+
+class WeightMap:
+    def __init__(self, model_dir: str, stream: Stream | None = None):
+        self.h = qmm_weight_map(None)
+        s = _stream(stream)
+        rc = lib.qmm_weights_load(byref(self.h), str(model_dir).encode(), s.h)
+        if rc:
+            raise QmmError(f"weights_load: {WE.get(rc, rc)}: {take_error()}")
+
+    def get(self, name: str) -> Array | None:
+        h = lib.qmm_weights_get(self.h, name.encode())
+        if not h.ctx:
+            return None
+        a = Array(qmm_array(None))
+        a.h = h
+        a.free = lambda: None  # borrowed: the map owns it
+        return a
+
+    def __len__(self):
+        return lib.qmm_weights_count(self.h)
+
+    @property
+    def quant(self):
+        q = lib.qmm_weights_quant(self.h)
+        return {QUANT_NONE: "none", QUANT_MXFP8: "mxfp8", QUANT_NVFP4: "nvfp4"}[q.mode], q.group_size, q.bits
+
+    def named_linear_q(self, x: Array, name: str, stream: Stream | None = None) -> Array:
+        res = Array()
+        rc = lib.qmm_named_linear_q(byref(res.h), self.h, x.h, name.encode(), _stream(stream).h)
+        if rc:
+            raise QmmError(f"named_linear_q: {WE.get(rc, rc)}: {take_error()}")
+        return res
+
+    def __del__(self):
+        try:
+            if self.h.ctx:
+                lib.qmm_weights_free(self.h)
+        except Exception:
+            pass
+
+
+def declared_symbols() -> list[str]:
+    """Every function the public header declares."""
+    import re
+
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qmm_[a-z0-9_]+)\s*\(", text)) - {"qmm_error_handler_func"})
