@@ -1,0 +1,268 @@
+// mxfp8 prefill GEMM on the gfx950 scaled fp8 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4).
+//
+// y[M, N] = x[M, K] @ deq(W)[N, K].T, W in mxfp8 (E4M3 bytes, one E8M0 scale per 32).
+//
+// The MFMA takes both operands in an 8-bit format with one E8M0 scale per row
+// and 32-wide K block -- exactly the mxfp8 weight layout, consumed raw.  x is
+// bf16 (8 significant bits); one E4M3 pass would keep 4 and miss the output
+// tolerance, so a pre-pass splits x per 32-block into
+//     x = hi * 2^(sh-127) + lo * 2^(sl-127)      (hi, lo E4M3; sh, sl E8M0)
+// with the scale chosen as 2^ceil(log2(amax/448)) (no element is clamped).
+// bf16's 8 bits fit in two 4-bit E4M3 significands, so the split is exact
+// except for elements below ~2^-9 of their block's max.  The GEMM then issues
+// two scaled MFMAs (hi, lo) per weight fragment into the same accumulator:
+// the weight tile is loaded once, the MFMA work doubles.
+//
+// Tiling: 256 threads (4 waves, 2 x 2), block tile 256 (x rows) x 256 (W rows),
+// K step 64, LDS double-buffered (rows padded to 80 bytes: conflict-free
+// 16-byte fragment reads), one barrier per K step; each wave owns 128 x 128
+// as 4 x 4 32x32 accumulators.
+#include "qmm_device.h"
+#include "qmm_launch.h"
+
+namespace qmm {
+
+// ---------------------------------------------------------------- x split pre-pass
+
+// Nearest E4M3 code to v >= 0 whose magnitude is at most 448 (ties to even).
+__device__ __forceinline__ uint32_t e4m3_rne_le448(float v) {
+  if (!(v > 0.f)) return 0u;
+  int e = (int)((__float_as_uint(v) >> 23) & 0xFF) - 127;
+  if (v < 0x1p-126f) e = -127;
+  int q = e - 3;
+  if (q < -9) q = -9;
+  float r = __builtin_ldexpf(__builtin_rintf(__builtin_ldexpf(v, -q)), q);
+  if (r > 448.f) r = 448.f;
+  if (r < 0x1p-6f) return (uint32_t)__builtin_ldexpf(r, 9);
+  uint32_t u = __float_as_uint(r);
+  return ((((u >> 23) & 0xFF) - 120u) << 3) | ((u >> 20) & 7u);
+}
+
+// Smallest t with 448 * 2^t >= amax (amax > 0, finite), clamped to the E8M0 range.
+__device__ __forceinline__ int ceil_scale_exp(float amax) {
+  uint32_t u = __float_as_uint(amax);
+  int e = (int)((u >> 23) & 0xFF);
+  int fl = e - 127;
+  uint32_t mant = u & 0x7FFFFFu;
+  if (e == 0) {  // f32 subnormal
+    fl = 31 - __builtin_clz(mant) - 149;
+    mant = (mant << (__builtin_clz(mant) - 8)) & 0x7FFFFFu;
+  }
+  int t = fl - 8;
+  if (mant > 0x600000u) t += 1;  // significand > 1.75: 448 * 2^(fl-8) < amax
+  if (t < -127) t = -127;
+  if (t > 127) t = 127;
+  return t;
+}
+
+// One thread per (row, 32-block).
+__global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict__ x, int64_t rows, int K,
+                                                      uint8_t *__restrict__ xh, uint8_t *__restrict__ xl,
+                                                      uint8_t *__restrict__ sh, uint8_t *__restrict__ sl) {
+  const int nb = K >> 5;
+  const int64_t total = rows * nb;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / nb;
+    const int b = (int)(i % nb);
+    const uint16_t *src = x + r * K + b * 32;
+    float v[32];
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint4 q = ((const uint4 *)src)[j];
+      uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        v[8 * j + 2 * t] = __uint_as_float(w4[t] << 16);
+        v[8 * j + 2 * t + 1] = __uint_as_float(w4[t] & 0xFFFF0000u);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    uint32_t hw[8], lw[8];
+    int th = amax > 0.f ? ceil_scale_exp(amax) : -127;
+    float rmax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      float p = __builtin_ldexpf(v[j], -th);
+      uint32_t c = e4m3_rne_le448(fabsf(p));
+      float back = __builtin_ldexpf(e4m3_to_f32_int(c), th);
+      float res = fabsf(v[j]) - back;  // exact: back shares v's leading bits
+      v[j] = signbit(v[j]) ? -res : res;
+      rmax = fmaxf(rmax, res < 0.f ? -res : res);
+      if (signbit(p) && c) c |= 0x80u;
+      if ((j & 3) == 0) hw[j >> 2] = 0u;
+      hw[j >> 2] |= c << (8 * (j & 3));
+    }
+    int tl = rmax > 0.f ? ceil_scale_exp(rmax) : -127;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      float p = __builtin_ldexpf(v[j], -tl);
+      uint32_t c = e4m3_rne_le448(fabsf(p));
+      if (signbit(p) && c) c |= 0x80u;
+      if ((j & 3) == 0) lw[j >> 2] = 0u;
+      lw[j >> 2] |= c << (8 * (j & 3));
+    }
+    uint4 *dh = (uint4 *)(xh + r * K + b * 32);
+    uint4 *dl = (uint4 *)(xl + r * K + b * 32);
+    dh[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    dh[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    dl[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    dl[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+    sh[r * nb + b] = (uint8_t)(th + 127);
+    sl[r * nb + b] = (uint8_t)(tl + 127);
+  }
+}
+
+// ---------------------------------------------------------------- GEMM
+
+namespace {
+constexpr int F_BM = 256, F_BN = 256, F_BK = 64, F_PITCH = 80;  // bytes per LDS row
+constexpr int F_TILE = 256 * F_PITCH;                            // one operand tile
+}  // namespace
+
+struct Fp8Smem {
+  uint8_t a_hi[2][F_TILE];
+  uint8_t a_lo[2][F_TILE];
+  uint8_t b[2][F_TILE];
+  uint8_t s_hi[2][256 * 2];
+  uint8_t s_lo[2][256 * 2];
+  uint8_t s_b[2][256 * 2];
+};
+
+__global__ __launch_bounds__(256) void gemm_mxfp8_kernel(const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl,
+                                                         const uint8_t *__restrict__ sh, const uint8_t *__restrict__ sl,
+                                                         const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
+                                                         uint16_t *__restrict__ y, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+  Fp8Smem &sm = *reinterpret_cast<Fp8Smem *>(smem_raw);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * F_BM, n0 = blockIdx.x * F_BN;
+  const int nb = K >> 5;  // scale bytes per row
+  const int steps = K / F_BK;
+
+  // loader mapping: 16-byte chunk c = tid + 256*j (j < 4): row c>>2, part c&3
+  uint4 ra_h[4], ra_l[4], rb[4];
+  uint16_t rs_h, rs_l, rs_b;
+  const int srow = tid;  // scale loader: one row per thread, 2 bytes (two 32-blocks)
+  const int64_t sm_row = (int64_t)min(m0 + srow, M - 1), sn_row = (int64_t)min(n0 + srow, N - 1);
+
+  auto gload = [&](int step) {
+    const int k0 = step * F_BK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = tid + 256 * j, row = c >> 2, part = c & 3;
+      const int64_t mr = min(m0 + row, M - 1), nr = min(n0 + row, N - 1);
+      ra_h[j] = *(const uint4 *)(xh + mr * K + k0 + part * 16);
+      ra_l[j] = *(const uint4 *)(xl + mr * K + k0 + part * 16);
+      rb[j] = load_stream16(w + nr * K + k0 + part * 16);
+    }
+    rs_h = *(const uint16_t *)(sh + sm_row * nb + (k0 >> 5));
+    rs_l = *(const uint16_t *)(sl + sm_row * nb + (k0 >> 5));
+    rs_b = *(const uint16_t *)(sw + sn_row * nb + (k0 >> 5));
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = tid + 256 * j, row = c >> 2, part = c & 3;
+      *(uint4 *)(sm.a_hi[buf] + row * F_PITCH + part * 16) = ra_h[j];
+      *(uint4 *)(sm.a_lo[buf] + row * F_PITCH + part * 16) = ra_l[j];
+      *(uint4 *)(sm.b[buf] + row * F_PITCH + part * 16) = rb[j];
+    }
+    *(uint16_t *)(sm.s_hi[buf] + srow * 2) = rs_h;
+    *(uint16_t *)(sm.s_lo[buf] + srow * 2) = rs_l;
+    *(uint16_t *)(sm.s_b[buf] + srow * 2) = rs_b;
+  };
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int fr = lane & 31, fk = (lane >> 5) * 32;  // fragment row within 32, K offset (bytes)
+  for (int s = 0; s < steps; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < steps) gload(s + 1);
+    i32x8_t bfr[4];
+    int bsc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = wn * 128 + j * 32 + fr;
+      const uint4 *p = (const uint4 *)(sm.b[buf] + row * F_PITCH + fk);
+      uint4 u0 = p[0], u1 = p[1];
+      bfr[j] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+      bsc[j] = sm.s_b[buf][row * 2 + (lane >> 5)];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = wm * 128 + i * 32 + fr;
+      const uint4 *ph = (const uint4 *)(sm.a_hi[buf] + row * F_PITCH + fk);
+      const uint4 *pl = (const uint4 *)(sm.a_lo[buf] + row * F_PITCH + fk);
+      uint4 h0 = ph[0], h1 = ph[1], l0 = pl[0], l1 = pl[1];
+      i32x8_t ah = i32x8_t{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+      i32x8_t al = i32x8_t{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+      const int shv = sm.s_hi[buf][row * 2 + (lane >> 5)];
+      const int slv = sm.s_lo[buf][row * 2 + (lane >> 5)];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ah, bfr[j], acc[i][j], 0, 0, 0, shv, 0, bsc[j]);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al, bfr[j], acc[i][j], 0, 0, 0, slv, 0, bsc[j]);
+      }
+    }
+    if (s + 1 < steps) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = n0 + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * 128 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (row < M && col < N) y[(int64_t)row * N + col] = f32_to_bf16_rne(acc[i][j][v]);
+      }
+    }
+}
+
+bool gemm_mxfp8_ok(const QmmArgs &a) {
+  return a.mode == MXFP8 && !a.x_f32 && a.K % F_BK == 0 && a.K > 0 && a.M > 0 && a.N > 0;
+}
+
+size_t gemm_mxfp8_workspace(const QmmArgs &a) {
+  const size_t mk = (size_t)a.M * a.K;
+  return 2 * mk + 2 * (mk / 32) + 256;
+}
+
+hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
+  if (!gemm_mxfp8_ok(a)) return hipErrorInvalidValue;
+  const size_t mk = (size_t)a.M * a.K;
+  uint8_t *xh = (uint8_t *)ws, *xl = xh + mk, *sh = xl + mk, *sl = sh + mk / 32;
+  const int64_t blocks_needed = ((int64_t)a.M * (a.K / 32) + 255) / 256;
+  const int64_t sb = blocks_needed < 65536 ? blocks_needed : 65536;
+  hipLaunchKernelGGL(split_x_kernel, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (int64_t)a.M, a.K, xh, xl, sh,
+                     sl);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  static bool attr_set = false;
+  if (!attr_set) {
+    e = hipFuncSetAttribute((const void *)gemm_mxfp8_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)sizeof(Fp8Smem));
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  dim3 grid((a.N + F_BN - 1) / F_BN, (a.M + F_BM - 1) / F_BM);
+  hipLaunchKernelGGL(gemm_mxfp8_kernel, grid, dim3(256), sizeof(Fp8Smem), st, xh, xl, sh, sl, a.w, a.s,
+                     (uint16_t *)a.y, a.M, a.N, a.K);
+  return hipGetLastError();
+}
+
+}  // namespace qmm

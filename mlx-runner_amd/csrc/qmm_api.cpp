@@ -480,6 +480,11 @@ int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array sca
     e = launch_fill_zero(a.y, ya->nbytes(), st);
   } else if (a.M <= QMV_MAX_M) {
     e = (aligned && qmv_fast_ok(a)) ? launch_qmv(a, st) : launch_qmv_generic(a, st);
+  } else if (aligned && gemm_mxfp8_ok(a)) {
+    void *ws = nullptr;
+    if (alloc_device(&ws, gemm_mxfp8_workspace(a), st)) return finish(1);
+    e = launch_gemm_mxfp8(a, ws, st);
+    (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
   } else if (aligned && gemm_ok(a)) {
     e = launch_gemm(a, st);
   } else {

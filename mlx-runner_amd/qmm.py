@@ -59,6 +59,15 @@ WE = {101: "BadIndexJson", 102: "BadHeader", 103: "UnsupportedDtype", 104: "Unsu
       105: "MissingTensor", 106: "DuplicateTensor", 107: "NonstandardQuant", 108: "InconsistentQuant",
       109: "AffineUnsupported", 110: "IO", 111: "MissingWeight"}
 
+# torch ships its own libamdhip64.so (soname libamdhip64.so.7).  If libqmm.so
+# were loaded first, its NEEDED entry would pull /opt/rocm's copy and torch
+# would later load a second HIP runtime, which then sees no device.  Loading
+# torch first makes libqmm.so bind to the runtime already in the process.
+try:
+    import torch as _torch  # noqa: F401
+except ImportError:  # pure C-ABI use without torch: /opt/rocm's runtime is the only one
+    _torch = None
+
 lib = ctypes.CDLL(str(LIB_PATH))
 
 ERROR_HANDLER = ctypes.CFUNCTYPE(None, c_char_p, c_void_p)
@@ -288,7 +297,8 @@ def quantize(w: Array, mode: str, *, group_size=None, bits=None, stream: Stream 
 
 def linear(x: Array, w: Array, *, stream: Stream | None = None) -> Array:
     res = Array()
-    check(lib.qmm_linear(byref(res.h), x.h, w.h, _stream(stream).h), "linear")
+    s = _stream(stream)  # keep the wrapper alive across the call (its __del__ frees the handle)
+    check(lib.qmm_linear(byref(res.h), x.h, w.h, s.h), "linear")
     return res
 
 
@@ -342,7 +352,8 @@ class WeightMap:
 
     def named_linear_q(self, x: Array, name: str, stream: Stream | None = None) -> Array:
         res = Array()
-        rc = lib.qmm_named_linear_q(byref(res.h), self.h, x.h, name.encode(), _stream(stream).h)
+        s = _stream(stream)
+        rc = lib.qmm_named_linear_q(byref(res.h), self.h, x.h, name.encode(), s.h)
         if rc:
             raise QmmError(f"named_linear_q: {WE.get(rc, rc)}: {take_error()}")
         return res

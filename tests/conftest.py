@@ -3,6 +3,7 @@ import sys
 from pathlib import Path
 
 import pytest
+import torch  # noqa: F401  (first: the HIP runtime libqmm.so binds to is torch's)
 
 ROOT = Path(__file__).resolve().parents[1]
 PKG = ROOT / "mlx-runner_amd"
