@@ -13,10 +13,10 @@
 // two scaled MFMAs (hi, lo) per weight fragment into the same accumulator:
 // the weight tile is loaded once, the MFMA work doubles.
 //
-// Tiling: 256 threads (4 waves, 2 x 2), block tile 256 (x rows) x 256 (W rows),
+// Tiling: 512 threads (8 waves, 4 x 2), block tile 256 (x rows) x 256 (W rows),
 // K step 64, LDS double-buffered (rows padded to 80 bytes: conflict-free
-// 16-byte fragment reads), one barrier per K step; each wave owns 128 x 128
-// as 4 x 4 32x32 accumulators.
+// 16-byte fragment reads), one barrier per K step; each wave owns 64 x 128
+// as 2 x 4 32x32 accumulators.
 #include "qmm_device.h"
 #include "qmm_launch.h"
 
@@ -117,8 +117,9 @@ __global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict
 // ---------------------------------------------------------------- GEMM
 
 namespace {
-constexpr int F_BM = 256, F_BN = 256, F_BK = 64, F_PITCH = 80;  // bytes per LDS row
+constexpr int F_BM = 256, F_BN = 256, F_BK = 64, F_PITCH = 80;  // bytes per LDS row (64 + 16 pad)
 constexpr int F_TILE = 256 * F_PITCH;                            // one operand tile
+constexpr int F_THREADS = 512;                                   // 8 waves: 4 (M) x 2 (N)
 }  // namespace
 
 struct Fp8Smem {
@@ -130,54 +131,78 @@ struct Fp8Smem {
   uint8_t s_b[2][256 * 2];
 };
 
-__global__ __launch_bounds__(256) void gemm_mxfp8_kernel(const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl,
-                                                         const uint8_t *__restrict__ sh, const uint8_t *__restrict__ sl,
-                                                         const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
-                                                         uint16_t *__restrict__ y, int M, int N, int K) {
+// Tile order: the hardware hands workgroup b to XCD b % 8.  Each XCD gets a
+// contiguous run of tile indices, and tiles are numbered in groups of 4 M-tiles
+// walked down M first, so the ~32 blocks resident on one XCD cover a 4 x 8
+// patch of (x rows, W rows) and share those operand slabs in that XCD's L2.
+__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int *tm, int *tn) {
+  const int T = tiles_m * tiles_n;
+  const int base = T / 8, rem = T % 8;
+  const int x = b % 8, local = b / 8;
+  const int t = x * base + (x < rem ? x : rem) + local;
+  constexpr int G = 4;
+  const int group = t / (G * tiles_n);
+  const int first_m = group * G;
+  const int gm = (tiles_m - first_m) < G ? (tiles_m - first_m) : G;
+  const int idx = t - group * G * tiles_n;
+  *tm = first_m + idx % gm;
+  *tn = idx / gm;
+}
+
+__global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_kernel(
+    const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
+    const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
+    uint16_t *__restrict__ y, int M, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   Fp8Smem &sm = *reinterpret_cast<Fp8Smem *>(smem_raw);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * F_BM, n0 = blockIdx.x * F_BN;
+  const int wm = wave >> 1, wn = wave & 1;  // wave tile: rows wm*64 + [0,64), cols wn*128 + [0,128)
+  int tm, tn;
+  tile_of(blockIdx.x, (M + F_BM - 1) / F_BM, (N + F_BN - 1) / F_BN, &tm, &tn);
+  const int m0 = tm * F_BM, n0 = tn * F_BN;
   const int nb = K >> 5;  // scale bytes per row
   const int steps = K / F_BK;
 
-  // loader mapping: 16-byte chunk c = tid + 256*j (j < 4): row c>>2, part c&3
-  uint4 ra_h[4], ra_l[4], rb[4];
-  uint16_t rs_h, rs_l, rs_b;
-  const int srow = tid;  // scale loader: one row per thread, 2 bytes (two 32-blocks)
-  const int64_t sm_row = (int64_t)min(m0 + srow, M - 1), sn_row = (int64_t)min(n0 + srow, N - 1);
+  // loader: 16-byte chunk c = tid + 512*j (j < 2) of each 256 x 64 tile: row c>>2, part c&3
+  uint4 ra_h[2], ra_l[2], rb[2];
+  uint16_t rs0, rs1;  // tid < 256: x-hi scales (rs0) and W scales (rs1) of row tid; else x-lo scales of row tid-256
+  const int srow = tid & 255;
+  const int64_t sm_row = min(m0 + srow, M - 1), sn_row = min(n0 + srow, N - 1);
+  const uint8_t *s_src0 = (tid < 256 ? sh : sl) + sm_row * nb;
+  const uint8_t *s_src1 = sw + sn_row * nb;
 
   auto gload = [&](int step) {
     const int k0 = step * F_BK;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = tid + 256 * j, row = c >> 2, part = c & 3;
+    for (int j = 0; j < 2; ++j) {
+      const int c = tid + F_THREADS * j, row = c >> 2, part = c & 3;
       const int64_t mr = min(m0 + row, M - 1), nr = min(n0 + row, N - 1);
       ra_h[j] = *(const uint4 *)(xh + mr * K + k0 + part * 16);
       ra_l[j] = *(const uint4 *)(xl + mr * K + k0 + part * 16);
       rb[j] = load_stream16(w + nr * K + k0 + part * 16);
     }
-    rs_h = *(const uint16_t *)(sh + sm_row * nb + (k0 >> 5));
-    rs_l = *(const uint16_t *)(sl + sm_row * nb + (k0 >> 5));
-    rs_b = *(const uint16_t *)(sw + sn_row * nb + (k0 >> 5));
+    rs0 = *(const uint16_t *)(s_src0 + (k0 >> 5));
+    if (tid < 256) rs1 = *(const uint16_t *)(s_src1 + (k0 >> 5));
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = tid + 256 * j, row = c >> 2, part = c & 3;
+    for (int j = 0; j < 2; ++j) {
+      const int c = tid + F_THREADS * j, row = c >> 2, part = c & 3;
       *(uint4 *)(sm.a_hi[buf] + row * F_PITCH + part * 16) = ra_h[j];
       *(uint4 *)(sm.a_lo[buf] + row * F_PITCH + part * 16) = ra_l[j];
       *(uint4 *)(sm.b[buf] + row * F_PITCH + part * 16) = rb[j];
     }
-    *(uint16_t *)(sm.s_hi[buf] + srow * 2) = rs_h;
-    *(uint16_t *)(sm.s_lo[buf] + srow * 2) = rs_l;
-    *(uint16_t *)(sm.s_b[buf] + srow * 2) = rs_b;
+    if (tid < 256) {
+      *(uint16_t *)(sm.s_hi[buf] + srow * 2) = rs0;
+      *(uint16_t *)(sm.s_b[buf] + srow * 2) = rs1;
+    } else {
+      *(uint16_t *)(sm.s_lo[buf] + srow * 2) = rs0;
+    }
   };
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -186,48 +211,53 @@ __global__ __launch_bounds__(256) void gemm_mxfp8_kernel(const uint8_t *__restri
   gload(0);
   sstore(0);
   __syncthreads();
-  const int fr = lane & 31, fk = (lane >> 5) * 32;  // fragment row within 32, K offset (bytes)
+  // Operand layout of v_mfma_scale_f32_32x32x64_f8f6f4 (measured on gfx950): lane l
+  // holds row l%32; its bytes 0-15 are K 16*(l/32)+[0,16) of block 0 and bytes 16-31
+  // the same span of block 1 (K+32).  Its scale byte covers block l/32 of row l%32.
+  const int fr = lane & 31, fh = lane >> 5, fk = fh * 16;
   for (int s = 0; s < steps; ++s) {
     const int buf = s & 1;
     if (s + 1 < steps) gload(s + 1);
-    i32x8_t bfr[4];
-    int bsc[4];
+    i32x8_t ah[2], al[2];
+    int shv[2], slv[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = wm * 64 + i * 32 + fr;
+      const uint8_t *ph = sm.a_hi[buf] + row * F_PITCH + fk;
+      const uint8_t *pl = sm.a_lo[buf] + row * F_PITCH + fk;
+      const uint4 h0 = *(const uint4 *)ph, h1 = *(const uint4 *)(ph + 32);
+      const uint4 l0 = *(const uint4 *)pl, l1 = *(const uint4 *)(pl + 32);
+      ah[i] = i32x8_t{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+      al[i] = i32x8_t{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+      shv[i] = sm.s_hi[buf][row * 2 + fh];
+      slv[i] = sm.s_lo[buf][row * 2 + fh];
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = wn * 128 + j * 32 + fr;
-      const uint4 *p = (const uint4 *)(sm.b[buf] + row * F_PITCH + fk);
-      uint4 u0 = p[0], u1 = p[1];
-      bfr[j] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
-      bsc[j] = sm.s_b[buf][row * 2 + (lane >> 5)];
-    }
+      const uint8_t *p = sm.b[buf] + row * F_PITCH + fk;
+      const uint4 u0 = *(const uint4 *)p, u1 = *(const uint4 *)(p + 32);
+      const i32x8_t bfr = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+      const int bsc = sm.s_b[buf][row * 2 + fh];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wm * 128 + i * 32 + fr;
-      const uint4 *ph = (const uint4 *)(sm.a_hi[buf] + row * F_PITCH + fk);
-      const uint4 *pl = (const uint4 *)(sm.a_lo[buf] + row * F_PITCH + fk);
-      uint4 h0 = ph[0], h1 = ph[1], l0 = pl[0], l1 = pl[1];
-      i32x8_t ah = i32x8_t{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
-      i32x8_t al = i32x8_t{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
-      const int shv = sm.s_hi[buf][row * 2 + (lane >> 5)];
-      const int slv = sm.s_lo[buf][row * 2 + (lane >> 5)];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ah, bfr[j], acc[i][j], 0, 0, 0, shv, 0, bsc[j]);
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al, bfr[j], acc[i][j], 0, 0, 0, slv, 0, bsc[j]);
+      for (int i = 0; i < 2; ++i) {
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ah[i], bfr, acc[i][j], 0, 0, 0, shv[i], 0, bsc);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al[i], bfr, acc[i][j], 0, 0, 0, slv[i], 0, bsc);
       }
     }
     if (s + 1 < steps) sstore(buf ^ 1);
     __syncthreads();
   }
 
+  // epilogue: 32x32 accumulator element v of lane l is row 8*(v/4) + 4*(l/32) + v%4, col l%32
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = n0 + wn * 128 + j * 32 + (lane & 31);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * 128 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        const int row = m0 + wm * 64 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
         if (row < M && col < N) y[(int64_t)row * N + col] = f32_to_bf16_rne(acc[i][j][v]);
       }
     }
@@ -259,8 +289,8 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  dim3 grid((a.N + F_BN - 1) / F_BN, (a.M + F_BM - 1) / F_BM);
-  hipLaunchKernelGGL(gemm_mxfp8_kernel, grid, dim3(256), sizeof(Fp8Smem), st, xh, xl, sh, sl, a.w, a.s,
+  const int tiles = ((a.M + F_BM - 1) / F_BM) * ((a.N + F_BN - 1) / F_BN);
+  hipLaunchKernelGGL(gemm_mxfp8_kernel, dim3(tiles), dim3(F_THREADS), sizeof(Fp8Smem), st, xh, xl, sh, sl, a.w, a.s,
                      (uint16_t *)a.y, a.M, a.N, a.K);
   return hipGetLastError();
 }
