@@ -208,6 +208,258 @@ __global__ __launch_bounds__(64) void qmv_generic_kernel(const void *__restrict_
   }
 }
 
+// ---------------------------------------------------------------- bf16 decode kernel
+//
+// 512-thread blocks; wave w of block b owns rows n0 = (8b + w) * R ... + R.  K is
+// walked in segments of ISEG chunk iterations: every lane issues all R x ISEG
+// 16-byte weight loads (plus their scale bytes) of a segment at once, with the
+// next segment's loads in flight while the current one is computed.  x is staged
+// once per block in LDS, each chunk's x padded (64 -> 80 bytes for nvfp4, 32 -> 48
+// for mxfp8) so the 16-byte reads of consecutive lanes land in distinct banks; its
+// global loads are issued before the weight loads so that staging waits only for
+// them.  When M * K is too large for LDS, x is read from global (L1/L2).
+constexpr int QMV_WAVES = 8;
+
+template <int MODE>
+struct XLayout {
+  static constexpr int EPC = MODE == NVFP4 ? 32 : 16;     // elements per 16-byte weight chunk
+  static constexpr int XBYTES = EPC * 2;                  // bf16 x bytes per chunk
+  static constexpr int PITCH = MODE == NVFP4 ? 80 : 48;   // padded LDS bytes per chunk
+  static constexpr int PIECES = XBYTES / 16;              // uint4 pieces per chunk
+};
+
+inline size_t qmv_lds_bytes(int mode, int M, int K) {
+  const int C = mode == MXFP8 ? K / 16 : K / 32;
+  return (size_t)M * C * (mode == NVFP4 ? 80 : 48);
+}
+constexpr size_t QMV_LDS_MAX = 64 * 1024;
+
+template <int MODE, int M, int R, int ISEG, int XP, bool DB>
+__global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t *__restrict__ x,
+                                                                  const uint8_t *__restrict__ w,
+                                                                  const uint8_t *__restrict__ s,
+                                                                  uint16_t *__restrict__ y, int N, int K) {
+  using L = XLayout<MODE>;
+  constexpr int THREADS = 64 * QMV_WAVES;
+  constexpr bool XLDS = XP > 0;  // XP: x pieces staged per thread (2 or 4; 0: x read from global)
+  static_assert(XP == 0 || XP == 2 || XP == 4, "x staging supports 2 or 4 pieces per thread");
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * QMV_WAVES + wave) * R;
+  const int64_t row_bytes = (MODE == MXFP8) ? (int64_t)K : (int64_t)(K >> 1);
+  const int C = (int)(row_bytes >> 4);
+  const int spr = (MODE == MXFP8) ? (K >> 5) : (K >> 4);
+  const uint8_t *wrow[R];
+  const uint8_t *srow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = n0 + r < N ? n0 + r : N - 1;  // tail rows re-read row N-1; results dropped
+    wrow[r] = w + (int64_t)n * row_bytes;
+    srow[r] = s + (int64_t)n * spr;
+  }
+
+  // 1) x staging loads first: the LDS write below then waits only for these,
+  //    not for the weight loads issued after them.
+  const int pieces = M * C * L::PIECES;  // host guarantees pieces <= XP * THREADS
+  // x pieces are contiguous in global memory: piece p is (m, c, j) with p = (m * C + c) * PIECES + j
+  auto xload = [&](int k) __attribute__((always_inline)) {
+    const int p = threadIdx.x + THREADS * k;
+    return ((const uint4 *)x)[p < pieces ? p : pieces - 1];
+  };
+  uint4 xr0, xr1, xr2, xr3;
+  if constexpr (XLDS) {
+    xr0 = xload(0);
+    xr1 = xload(1);
+    if constexpr (XP > 2) {
+      xr2 = xload(2);
+      xr3 = xload(3);
+    }
+  }
+
+  // 2) weight loads of a segment: clamped addresses, no per-load branches
+  auto load_seg = [&](int seg, uint4 (&q)[ISEG][R], uint32_t (&sc)[ISEG][R]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < ISEG; ++i) {
+      int c = seg * 64 * ISEG + lane + 64 * i;
+      c = c < C ? c : C - 1;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        q[i][r] = load_stream16(wrow[r] + ((int64_t)c << 4));
+        sc[i][r] = (MODE == NVFP4) ? (uint32_t) * (const uint16_t *)(srow[r] + 2 * c) : (uint32_t)srow[r][c >> 1];
+      }
+    }
+  };
+
+  float acc[R][M];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+
+  auto compute_seg = [&](int seg, const uint4 (&q)[ISEG][R], const uint32_t (&sc)[ISEG][R]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < ISEG; ++i) {
+      const int craw = seg * 64 * ISEG + lane + 64 * i;
+      const bool valid = craw < C;
+      const int c = valid ? craw : C - 1;
+      constexpr int XW = L::XBYTES / 4;
+      uint32_t xw[M][XW];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+#pragma unroll
+        for (int j = 0; j < L::PIECES; ++j) {
+          const uint4 t = XLDS ? *(const uint4 *)(xs + (m * C + c) * L::PITCH + 16 * j)
+                               : ((const uint4 *)(x + (int64_t)m * K + (int64_t)c * L::EPC))[j];
+          xw[m][4 * j + 0] = t.x;
+          xw[m][4 * j + 1] = t.y;
+          xw[m][4 * j + 2] = t.z;
+          xw[m][4 * j + 3] = t.w;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t d[4] = {q[i][r].x, q[i][r].y, q[i][r].z, q[i][r].w};
+        if constexpr (MODE == NVFP4) {
+          bf16x2_t wb[16];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            wb[4 * j + 0] = fp4x2_to_bf16x2<0>(d[j]);
+            wb[4 * j + 1] = fp4x2_to_bf16x2<1>(d[j]);
+            wb[4 * j + 2] = fp4x2_to_bf16x2<2>(d[j]);
+            wb[4 * j + 3] = fp4x2_to_bf16x2<3>(d[j]);
+          }
+          const float s0 = __builtin_amdgcn_cvt_f32_fp8((int)sc[i][r], 0);
+          const float s1 = __builtin_amdgcn_cvt_f32_fp8((int)sc[i][r], 1);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            float g0 = 0.f, g1 = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) g0 = dot2_bf16(wb[j], xw[m][j], g0);
+#pragma unroll
+            for (int j = 8; j < 16; ++j) g1 = dot2_bf16(wb[j], xw[m][j], g1);
+            const float t = __builtin_fmaf(g1, s1, g0 * s0);
+            acc[r][m] += valid ? t : 0.f;
+          }
+        } else {
+          bf16x2_t wb[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            wb[2 * j + 0] = fp8x2_to_bf16x2<false>(d[j]);
+            wb[2 * j + 1] = fp8x2_to_bf16x2<true>(d[j]);
+          }
+          const float s0 = e8m0_to_f32(sc[i][r]);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            float g = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) g = dot2_bf16(wb[j], xw[m][j], g);
+            acc[r][m] += valid ? g * s0 : 0.f;
+          }
+        }
+      }
+    }
+  };
+
+  const int nseg = (C + 64 * ISEG - 1) / (64 * ISEG);
+  uint4 qa[ISEG][R], qb[DB ? ISEG : 1][R];
+  uint32_t sa[ISEG][R], sb[DB ? ISEG : 1][R];
+  load_seg(0, qa, sa);
+  if constexpr (DB) {
+    if (nseg > 1) load_seg(1, qb, sb);
+  }
+  if constexpr (XLDS) {
+    // piece (m, c, j) lands at (m * C + c) * PITCH + 16 j
+    auto xstore = [&](int k, const uint4 &v) __attribute__((always_inline)) {
+      const int p = threadIdx.x + THREADS * k;
+      if (p < pieces) {
+        const int mc = p / L::PIECES, j = p - mc * L::PIECES;
+        *(uint4 *)(xs + mc * L::PITCH + 16 * j) = v;
+      }
+    };
+    xstore(0, xr0);
+    xstore(1, xr1);
+    if constexpr (XP > 2) {
+      xstore(2, xr2);
+      xstore(3, xr3);
+    }
+    __syncthreads();
+  }
+  if constexpr (DB) {
+    // two segments in flight: compute one while the next one's loads land
+    for (int seg = 0; seg < nseg; seg += 2) {
+      compute_seg(seg, qa, sa);
+      if (seg + 2 < nseg) load_seg(seg + 2, qa, sa);
+      if (seg + 1 < nseg) {
+        compute_seg(seg + 1, qb, sb);
+        if (seg + 3 < nseg) load_seg(seg + 3, qb, sb);
+      }
+    }
+  } else {
+    for (int seg = 0; seg < nseg; ++seg) {
+      if (seg > 0) load_seg(seg, qa, sa);
+      compute_seg(seg, qa, sa);
+    }
+  }
+
+  float out = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float t = wave_sum(acc[r][m]);
+      out = (lane == r * M + m) ? t : out;
+    }
+  if (lane < R * M) {
+    const int r = lane / M, m = lane % M;
+    if (n0 + r < N) y[(int64_t)m * N + n0 + r] = f32_to_bf16_rne(out);
+  }
+}
+
+template <int MODE, int M, int R, int ISEG, bool DB>
+static hipError_t launch_qmv_bf16_t(const QmmArgs &a, hipStream_t st) {
+  const size_t lds = qmv_lds_bytes(MODE, M, a.K);
+  const int C = MODE == MXFP8 ? a.K / 16 : a.K / 32;
+  const int pieces = M * C * (MODE == NVFP4 ? 4 : 2);
+  constexpr int T = 64 * QMV_WAVES;
+  dim3 grid((a.N + R * QMV_WAVES - 1) / (R * QMV_WAVES));
+  const uint16_t *x = (const uint16_t *)a.x;
+  uint16_t *y = (uint16_t *)a.y;
+  if (lds <= QMV_LDS_MAX && pieces <= 2 * T)
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 2, DB>), grid, dim3(T), lds, st, x, a.w, a.s, y, a.N, a.K);
+  else if (lds <= QMV_LDS_MAX && pieces <= 4 * T)
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 4, DB>), grid, dim3(T), lds, st, x, a.w, a.s, y, a.N, a.K);
+  else
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 0, DB>), grid, dim3(T), 0, st, x, a.w, a.s, y, a.N, a.K);
+  return hipGetLastError();
+}
+
+// rows per wave: 2 at M = 1 (more waves in flight), 4 for M >= 2 (x reuse across rows)
+// Single-segment shapes only (C <= 320 chunks: nvfp4 K <= 10240, mxfp8 K <= 5120);
+// longer rows use the looping kernel above (measured faster there).
+template <int MODE, int M>
+static hipError_t launch_qmv_bf16_m(const QmmArgs &a, hipStream_t st) {
+  constexpr int R = M == 1 ? 1 : 2;
+  const int C = MODE == MXFP8 ? a.K / 16 : a.K / 32;
+  if (C <= 3 * 64) return launch_qmv_bf16_t<MODE, M, R, 3, false>(a, st);
+  return launch_qmv_bf16_t<MODE, M, R, 5, false>(a, st);
+}
+
+template <int MODE>
+static hipError_t launch_qmv_bf16(const QmmArgs &a, hipStream_t st) {
+  switch (a.M) {
+    case 1: return launch_qmv_bf16_m<MODE, 1>(a, st);
+    case 2: return launch_qmv_bf16_m<MODE, 2>(a, st);
+    case 3: return launch_qmv_bf16_m<MODE, 3>(a, st);
+    case 4: return launch_qmv_bf16_m<MODE, 4>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+static bool qmv_single_segment(const QmmArgs &a) {
+  const int C = a.mode == MXFP8 ? a.K / 16 : a.K / 32;
+  return a.M <= 4 && C <= 5 * 64;
+}
+
 template <int MODE, int M, int R, bool XF32>
 static hipError_t launch_qmv_t(const QmmArgs &a, hipStream_t st) {
   dim3 grid((a.N + R - 1) / R);
@@ -237,6 +489,8 @@ bool qmv_fast_ok(const QmmArgs &a) {
 
 hipError_t launch_qmv(const QmmArgs &a, hipStream_t st) {
   if (!qmv_fast_ok(a)) return hipErrorInvalidValue;
+  if (!a.x_f32 && qmv_single_segment(a))
+    return a.mode == MXFP8 ? launch_qmv_bf16<MXFP8>(a, st) : launch_qmv_bf16<NVFP4>(a, st);
   if (a.mode == MXFP8) return a.x_f32 ? launch_qmv_mode<MXFP8, true>(a, st) : launch_qmv_mode<MXFP8, false>(a, st);
   return a.x_f32 ? launch_qmv_mode<NVFP4, true>(a, st) : launch_qmv_mode<NVFP4, false>(a, st);
 }
