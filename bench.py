@@ -125,6 +125,9 @@ def main():
     ap.add_argument("--config", default=DEFAULT, choices=sorted(CONFIGS))
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="instead of the workload, run K plain 512 MiB -> 512 MiB copy kernels (torch.neg on "
+                         "float32) so HBM counters (FETCH_SIZE / WRITE_SIZE) can be scaled to known bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this path runs on a single MI355X); got --gpus {args.gpus}",
@@ -135,6 +138,18 @@ def main():
     import torch
 
     import qmm as Q
+
+    if args.copy_calibration:
+        n = 128 << 20  # float32 elements: 512 MiB read + 512 MiB written per launch
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_kernel": "torch.neg float32", "bytes_read_per_launch": n * 4,
+                          "bytes_written_per_launch": n * 4, "launches": args.steps}), flush=True)
+        return
 
     cfg = CONFIGS[args.config]
     mode, M, N, K = cfg["mode"], cfg["M"], cfg["N"], cfg["K"]

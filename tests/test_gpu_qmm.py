@@ -120,6 +120,27 @@ def test_reference_qmm_case_exact(mode):
 
 
 @pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+def test_reference_qmm_case_golden(mode):
+    """The committed fixture of the same case: packed words and scales from the
+    format definitions; the GPU quantizer, dequant and qmm must reproduce them."""
+    import json
+    from pathlib import Path
+
+    g = json.loads((Path(__file__).resolve().parent / "golden" / "reference_qmm_case.json").read_text())
+    gm = g["modes"][mode]
+    W, x, y = (np.array(g[k], np.float32) for k in ("W", "x", "y"))
+    wq, s = Q.quantize(Q.Array.from_numpy(W, Q.FLOAT32), mode)
+    assert np.array_equal(wq.numpy(), np.array(gm["w"], np.uint32))
+    assert np.array_equal(s.numpy(), np.array(gm["scales"], np.uint8))
+    wg = Q.Array.from_numpy(np.array(gm["w"], np.uint32), Q.UINT32)
+    sg = Q.Array.from_numpy(np.array(gm["scales"], np.uint8), Q.UINT8)
+    assert np.array_equal(Q.dequantize(wg, sg, mode, dtype=Q.FLOAT32).numpy(), W)
+    assert np.array_equal(Q.quantized_matmul(Q.Array.from_numpy(x, Q.FLOAT32), wg, sg, mode).numpy(), y)
+    yb = Q.quantized_matmul(Q.Array.from_numpy(bf16(x), Q.BFLOAT16), wg, sg, mode).numpy()
+    assert np.array_equal(f32(yb), y)
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("N,K", [(256, 512), (61, 1536), (48, 5120), (37, 96)])
 def test_decode_matches_oracle(mode, M, N, K):
