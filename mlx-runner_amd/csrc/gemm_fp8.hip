@@ -263,6 +263,184 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_kernel(
     }
 }
 
+// ---------------------------------------------------------------- pipelined GEMM (K % 128 == 0)
+//
+// Same block tile (256 x 256, 8 waves of 64 x 128) and MFMA as above, with the
+// operand traffic moved off the VGPRs:
+//   * every operand byte goes global -> LDS directly (global_load_lds: lane i
+//     of a wave writes bytes [16 i, 16 i + 16) of the wave's 1 KiB destination,
+//     [4 i, 4 i + 4) for the dword form), into a 3-stage ring: the loads of step
+//     s + 2 are issued while step s computes, so a load has two steps (~2 x 2048
+//     MFMA cycles) to land;
+//   * the DMA is issued from inline assembly and waited for explicitly
+//     (s_waitcnt vmcnt), so no compiler-inserted wait serialises the ring;
+//   * a tile is 256 rows x 64 bytes, unpadded; 16-byte slot p of row r is stored
+//     at slot p ^ swz(r), swz(r) = ((r >> 1) ^ (r >> 2)) & 3, so the fragment
+//     reads of 8 (or 16) consecutive rows at one slot hit distinct banks;
+//   * scales: per stage, the dword holding each row's 4 E8M0 bytes of the step
+//     pair (the step uses 2 of them) for x hi, x lo and W;
+//   * one barrier per step; each wave issues exactly 8 DMAs per step (6 tile,
+//     2 scale), the count the waits are written for.
+namespace {
+constexpr int P_BK = 64, P_STAGES = 3, P_TILE = 256 * P_BK;  // 16 KiB per operand tile
+constexpr int P_SCALES = 4 * 1024;                           // x hi, x lo, W scale dwords + 1 KiB spare
+constexpr int P_STAGE = 3 * P_TILE + P_SCALES;               // 52 KiB
+constexpr size_t P_LDS = (size_t)P_STAGES * P_STAGE;         // 156 KiB
+}  // namespace
+
+__device__ __forceinline__ int p_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// LDS DMA: lane i's 16 (4) bytes at g land at LDS byte l + 16 i (4 i); l must be wave-uniform.
+__device__ __forceinline__ void p_dma16(const void *g, uint32_t l) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(l), "v"(g) : "memory", "m0");
+}
+__device__ __forceinline__ void p_dma4(const void *g, uint32_t l) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(l), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// Wait until this wave's DMAs of the next stage have landed (at most 8 of the
+// stage after it still in flight, or none) and its LDS reads of this stage are
+// done (the stage is refilled two steps later), then barrier the workgroup.
+__device__ __forceinline__ void p_wait8_barrier() {
+  asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+__device__ __forceinline__ void p_wait0_barrier() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ i32x8_t p_frag(const uint8_t *base, int off) {
+  const uint4 u0 = *(const uint4 *)(base + off), u1 = *(const uint4 *)(base + (off ^ 32));
+  return i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+}
+
+__global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
+    const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
+    const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
+    uint16_t *__restrict__ y, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  int tm, tn;
+  tile_of(blockIdx.x, (M + F_BM - 1) / F_BM, (N + F_BN - 1) / F_BN, &tm, &tn);
+  const int m0 = tm * F_BM, n0 = tn * F_BN;
+  const int nb = K >> 5;
+  const int steps = K / P_BK;
+
+  // tile DMA: wave-instruction t (0, 1) of this wave fills LDS slots q = (8 t + wave) * 64 + lane
+  const uint8_t *ga_h[2], *ga_l[2], *gb[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int q = (8 * t + wave) * 64 + lane, row = q >> 2, part = (q & 3) ^ p_swz(row);
+    const int64_t ar = min(m0 + row, M - 1), br = min(n0 + row, N - 1);
+    ga_h[t] = xh + ar * K + part * 16;
+    ga_l[t] = xl + ar * K + part * 16;
+    gb[t] = w + br * K + part * 16;
+  }
+  // scale DMA: wave-instruction t = 2 wave + {0, 1} of 16 loads row (t % 4) * 64 + lane of
+  // tensor t / 4 (x hi, x lo, W; the 4th re-reads x hi into the spare KiB)
+  const uint8_t *gs[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int t = 2 * wave + h, tensor = t >> 2, row = (t & 3) * 64 + lane;
+    const uint8_t *src = tensor == 1 ? sl : tensor == 2 ? sw : sh;
+    const int base = tensor == 2 ? n0 : m0, lim = tensor == 2 ? N : M;
+    gs[h] = src + (int64_t)min(base + row, lim - 1) * nb;
+  }
+  auto issue = [&](int s) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + (uint32_t)((s % P_STAGES) * P_STAGE);
+    const int k0 = s * P_BK;
+    p_dma16(ga_h[0] + k0, st + wave * 1024);
+    p_dma16(ga_h[1] + k0, st + (8 + wave) * 1024);
+    p_dma16(ga_l[0] + k0, st + P_TILE + wave * 1024);
+    p_dma16(ga_l[1] + k0, st + P_TILE + (8 + wave) * 1024);
+    p_dma16(gb[0] + k0, st + 2 * P_TILE + wave * 1024);
+    p_dma16(gb[1] + k0, st + 2 * P_TILE + (8 + wave) * 1024);
+    const int so = 4 * (s >> 1);  // dword of the step pair
+    p_dma4(gs[0] + so, st + 3 * P_TILE + (2 * wave) * 256);
+    p_dma4(gs[1] + so, st + 3 * P_TILE + (2 * wave + 1) * 256);
+  };
+
+  // fragment geometry (32x32x64 operand layout: lane l holds row l % 32, K bytes 16 (l / 32) + [0, 16) and +32)
+  const int fr = lane & 31, fh = lane >> 5;
+  int oa[2], ob[4], osa[2], osb[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = wm * 64 + i * 32 + fr;
+    oa[i] = r * P_BK + 16 * (fh ^ p_swz(r));
+    osa[i] = 3 * P_TILE + r * 4 + fh;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = wn * 128 + j * 32 + fr;
+    ob[j] = r * P_BK + 16 * (fh ^ p_swz(r));
+    osb[j] = 3 * P_TILE + 2 * 1024 + r * 4 + fh;
+  }
+
+  f32x16_t acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  issue(0);
+  if (steps > 1) {
+    issue(1);
+    p_wait8_barrier();
+  } else {
+    p_wait0_barrier();
+  }
+  for (int s = 0; s < steps; ++s) {
+    if (s + 2 < steps) issue(s + 2);
+    const uint8_t *st = lds + (s % P_STAGES) * P_STAGE;
+    const int sb = 2 * (s & 1);  // byte of the pair dword: block fh of this step
+    i32x8_t ah[2], al[2];
+    int shv[2], slv[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      ah[i] = p_frag(st, oa[i]);
+      al[i] = p_frag(st + P_TILE, oa[i]);
+      shv[i] = st[osa[i] + sb];
+      slv[i] = st[osa[i] + 1024 + sb];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const i32x8_t bfr = p_frag(st + 2 * P_TILE, ob[j]);
+      const int bsc = st[osb[j] + sb];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ah[i], bfr, acc[i][j], 0, 0, 0, shv[i], 0, bsc);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al[i], bfr, acc[i][j], 0, 0, 0, slv[i], 0, bsc);
+      }
+    }
+    if (s + 2 < steps) p_wait8_barrier();
+    else p_wait0_barrier();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = n0 + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * 64 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (row < M && col < N) y[(int64_t)row * N + col] = f32_to_bf16_rne(acc[i][j][v]);
+      }
+    }
+}
+
+// K % 128: whole step pairs, so every scale dword (4 bytes of a row) lies inside the
+// row and is 4-byte aligned; the DMA sources must be 16- / 4-byte aligned.
+static bool gemm_mxfp8_pipe_ok(const QmmArgs &a) {
+  return a.K % 128 == 0 && (uintptr_t)a.w % 16 == 0 && (uintptr_t)a.s % 4 == 0;
+}
+
 bool gemm_mxfp8_ok(const QmmArgs &a) {
   return a.mode == MXFP8 && !a.x_f32 && a.K % F_BK == 0 && a.K > 0 && a.M > 0 && a.N > 0;
 }
@@ -282,6 +460,19 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
                      sl);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  const int tiles = ((a.M + F_BM - 1) / F_BM) * ((a.N + F_BN - 1) / F_BN);
+  if (gemm_mxfp8_pipe_ok(a)) {
+    static bool pipe_attr_set = false;
+    if (!pipe_attr_set) {
+      e = hipFuncSetAttribute((const void *)gemm_mxfp8_pipe_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)P_LDS);
+      if (e != hipSuccess) return e;
+      pipe_attr_set = true;
+    }
+    hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel, dim3(tiles), dim3(F_THREADS), P_LDS, st, xh, xl, sh, sl, a.w, a.s,
+                       (uint16_t *)a.y, a.M, a.N, a.K);
+    return hipGetLastError();
+  }
   static bool attr_set = false;
   if (!attr_set) {
     e = hipFuncSetAttribute((const void *)gemm_mxfp8_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -289,7 +480,6 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  const int tiles = ((a.M + F_BM - 1) / F_BM) * ((a.N + F_BN - 1) / F_BN);
   hipLaunchKernelGGL(gemm_mxfp8_kernel, dim3(tiles), dim3(F_THREADS), sizeof(Fp8Smem), st, xh, xl, sh, sl, a.w, a.s,
                      (uint16_t *)a.y, a.M, a.N, a.K);
   return hipGetLastError();
