@@ -17,6 +17,8 @@
 // K step 64, LDS double-buffered (rows padded to 80 bytes: conflict-free
 // 16-byte fragment reads), one barrier per K step; each wave owns 64 x 128
 // as 2 x 4 32x32 accumulators.
+#include <type_traits>
+
 #include "qmm_device.h"
 #include "qmm_launch.h"
 
@@ -55,7 +57,23 @@ __device__ __forceinline__ int ceil_scale_exp(float amax) {
   return t;
 }
 
-// One thread per (row, 32-block).
+// LDS / pre-tiled operand swizzle of the pipelined GEMM: 16-byte slot p of row r
+// (64 bytes of one K step) is stored at slot p ^ p_swz(r) of the row.
+__host__ __device__ __forceinline__ int p_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+// Scale byte of (row r, 32-block b) in the tile-major layout the pipelined GEMM
+// loads: [r / 256][b / 4][r % 256][b % 4], i.e. for each 256-row tile and pair of
+// 64-wide K steps, 256 contiguous dwords (one per row).  Needs K % 128 == 0.
+__host__ __device__ __forceinline__ int64_t packed_scale_index(int64_t r, int b, int K) {
+  return (((r >> 8) * (K >> 7) + (b >> 2)) * 256 + (r & 255)) * 4 + (b & 3);
+}
+
+// One thread per (row, 32-block).  PACKED: scales in the tile-major layout above
+// and hi / lo pre-tiled the way the pipelined GEMM's LDS holds them: for each
+// 256-row tile and 64-wide K step, one contiguous 16 KiB block of 1024 slots of
+// 16 bytes, slot 4 r + (p ^ p_swz(r)) holding bytes [16 p, 16 p + 16) of row r's
+// step.  Otherwise row-major [rows, K] and [rows, K / 32].
+template <bool PACKED>
 __global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict__ x, int64_t rows, int K,
                                                       uint8_t *__restrict__ xh, uint8_t *__restrict__ xl,
                                                       uint8_t *__restrict__ sh, uint8_t *__restrict__ sl) {
@@ -103,14 +121,23 @@ __global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict
       if ((j & 3) == 0) lw[j >> 2] = 0u;
       lw[j >> 2] |= c << (8 * (j & 3));
     }
-    uint4 *dh = (uint4 *)(xh + r * K + b * 32);
-    uint4 *dl = (uint4 *)(xl + r * K + b * 32);
-    dh[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    dh[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-    dl[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    dl[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
-    sh[r * nb + b] = (uint8_t)(th + 127);
-    sl[r * nb + b] = (uint8_t)(tl + 127);
+    int64_t o0, o1;  // byte offsets of the block's two 16-byte halves
+    if (PACKED) {
+      const int64_t blk = ((r >> 8) * (K >> 6) + (b >> 1)) * 16384;
+      const int rr = (int)(r & 255), p0 = 2 * (b & 1);
+      o0 = blk + 16 * (4 * rr + (p0 ^ p_swz(rr)));
+      o1 = blk + 16 * (4 * rr + ((p0 + 1) ^ p_swz(rr)));
+    } else {
+      o0 = r * K + b * 32;
+      o1 = o0 + 16;
+    }
+    *(uint4 *)(xh + o0) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(xh + o1) = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    *(uint4 *)(xl + o0) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    *(uint4 *)(xl + o1) = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+    const int64_t so = PACKED ? packed_scale_index(r, b, K) : r * nb + b;
+    sh[so] = (uint8_t)(th + 127);
+    sl[so] = (uint8_t)(tl + 127);
   }
 }
 
@@ -288,7 +315,21 @@ constexpr int P_STAGE = 3 * P_TILE + P_SCALES;               // 52 KiB
 constexpr size_t P_LDS = (size_t)P_STAGES * P_STAGE;         // 156 KiB
 }  // namespace
 
-__device__ __forceinline__ int p_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+// W scales [N, K / 32] (row-major, as loaded) -> the tile-major layout of
+// packed_scale_index, one dword (4 blocks of one row) per thread.  Rows past N
+// (up to the next multiple of 256) repeat row N - 1; their outputs are dropped.
+__global__ __launch_bounds__(256) void repack_scales_kernel(const uint8_t *__restrict__ s, int64_t N, int K,
+                                                            uint32_t *__restrict__ out) {
+  const int nb = K >> 5, pairs = K >> 7;
+  const int64_t total = ((N + 255) >> 8) * pairs * 256;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rr = i & 255, tu = i >> 8;
+    const int64_t tile = tu / pairs, u = tu % pairs;
+    const int64_t r = min(tile * 256 + rr, N - 1);
+    out[i] = *(const uint32_t *)(s + r * nb + 4 * u);
+  }
+}
 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
@@ -309,6 +350,8 @@ __device__ __forceinline__ void p_wait8_barrier() {
 __device__ __forceinline__ void p_wait0_barrier() {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+__device__ __forceinline__ void p_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void p_barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
 __device__ __forceinline__ i32x8_t p_frag(const uint8_t *base, int off) {
   const uint4 u0 = *(const uint4 *)(base + off), u1 = *(const uint4 *)(base + (off ^ 32));
@@ -327,39 +370,43 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
   int tm, tn;
   tile_of(blockIdx.x, (M + F_BM - 1) / F_BM, (N + F_BN - 1) / F_BN, &tm, &tn);
   const int m0 = tm * F_BM, n0 = tn * F_BN;
-  const int nb = K >> 5;
   const int steps = K / P_BK;
 
   // tile DMA: wave-instruction t (0, 1) of this wave fills LDS slots q = (8 t + wave) * 64 + lane
+  // (x hi / lo are pre-tiled: the tile's step block is contiguous, in LDS order;
+  // W is row-major: slot q holds row q >> 2, 16-byte part (q & 3) ^ swz(row))
   const uint8_t *ga_h[2], *ga_l[2], *gb[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int q = (8 * t + wave) * 64 + lane, row = q >> 2, part = (q & 3) ^ p_swz(row);
-    const int64_t ar = min(m0 + row, M - 1), br = min(n0 + row, N - 1);
-    ga_h[t] = xh + ar * K + part * 16;
-    ga_l[t] = xl + ar * K + part * 16;
-    gb[t] = w + br * K + part * 16;
+    const int64_t xo = (int64_t)tm * steps * P_TILE + q * 16;
+    ga_h[t] = xh + xo;
+    ga_l[t] = xl + xo;
+    gb[t] = w + (int64_t)min(n0 + row, N - 1) * K + part * 16;
   }
-  // scale DMA: wave-instruction t = 2 wave + {0, 1} of 16 loads row (t % 4) * 64 + lane of
-  // tensor t / 4 (x hi, x lo, W; the 4th re-reads x hi into the spare KiB)
+  // scale DMA: wave-instruction t = 2 wave + {0, 1} of 16 copies the 256 contiguous
+  // bytes [(t % 4) * 256, + 256) of the step pair's 1 KiB block of tensor t / 4 (x hi,
+  // x lo, W, all tile-major; the 4th re-reads x hi into the spare KiB)
   const uint8_t *gs[2];
+  const int pairs = K >> 7;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int t = 2 * wave + h, tensor = t >> 2, row = (t & 3) * 64 + lane;
     const uint8_t *src = tensor == 1 ? sl : tensor == 2 ? sw : sh;
-    const int base = tensor == 2 ? n0 : m0, lim = tensor == 2 ? N : M;
-    gs[h] = src + (int64_t)min(base + row, lim - 1) * nb;
+    const int tile = tensor == 2 ? tn : tm;
+    gs[h] = src + ((int64_t)tile * pairs * 256 + row) * 4;
   }
   auto issue = [&](int s) __attribute__((always_inline)) {
     const uint32_t st = lds0 + (uint32_t)((s % P_STAGES) * P_STAGE);
     const int k0 = s * P_BK;
-    p_dma16(ga_h[0] + k0, st + wave * 1024);
-    p_dma16(ga_h[1] + k0, st + (8 + wave) * 1024);
-    p_dma16(ga_l[0] + k0, st + P_TILE + wave * 1024);
-    p_dma16(ga_l[1] + k0, st + P_TILE + (8 + wave) * 1024);
+    const int64_t xs = (int64_t)s * P_TILE;
+    p_dma16(ga_h[0] + xs, st + wave * 1024);
+    p_dma16(ga_h[1] + xs, st + (8 + wave) * 1024);
+    p_dma16(ga_l[0] + xs, st + P_TILE + wave * 1024);
+    p_dma16(ga_l[1] + xs, st + P_TILE + (8 + wave) * 1024);
     p_dma16(gb[0] + k0, st + 2 * P_TILE + wave * 1024);
     p_dma16(gb[1] + k0, st + 2 * P_TILE + (8 + wave) * 1024);
-    const int so = 4 * (s >> 1);  // dword of the step pair
+    const int so = 1024 * (s >> 1);  // the step pair's 1 KiB block
     p_dma4(gs[0] + so, st + 3 * P_TILE + (2 * wave) * 256);
     p_dma4(gs[1] + so, st + 3 * P_TILE + (2 * wave + 1) * 256);
   };
@@ -388,19 +435,32 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
+  // Ping-pong: waves 0-3 (group 0) and 4-7 (group 1) put one wave of each group on
+  // every SIMD.  Barrier intervals alternate: in each, one group runs the 16 MFMAs
+  // of its step while the other issues its DMAs and reads its next fragments, so
+  // the MFMA pipe of every SIMD always has a wave feeding it.  Group 0 computes
+  // step k in interval 2k + 1, group 1 in 2k + 2.  DMA(k + 2) overwrites the
+  // stage group 1 read in interval 2k - 1, and is issued in the loading interval
+  // of step k (2k, 2k + 1); at the barrier that ends interval 2k + 1 every wave
+  // waits for its DMA(k + 1) (only DMA(k + 2), 8 loads, may remain), so stage
+  // k + 1 is whole before group 0 reads it in interval 2k + 2.
+  const int grp = wave >> 2;
   issue(0);
-  if (steps > 1) {
-    issue(1);
-    p_wait8_barrier();
-  } else {
-    p_wait0_barrier();
-  }
-  for (int s = 0; s < steps; ++s) {
-    if (s + 2 < steps) issue(s + 2);
+  if (steps > 1) issue(1);
+  if (steps > 1) p_wait8_barrier();
+  else p_wait0_barrier();
+
+  // one step of a group: loading interval (DMAs of step s + 2 if DMA, fragments of
+  // step s), barrier, computing interval, barrier.  Each call is one basic block, so
+  // the scheduling barriers keep the MFMAs inside their interval.
+  auto pp_step = [&](auto grp_c, auto dma_c, int s) __attribute__((always_inline)) {
+    constexpr int GRP = decltype(grp_c)::value;
+    constexpr bool DMA = decltype(dma_c)::value;
+    if constexpr (DMA) issue(s + 2);
     const uint8_t *st = lds + (s % P_STAGES) * P_STAGE;
     const int sb = 2 * (s & 1);  // byte of the pair dword: block fh of this step
-    i32x8_t ah[2], al[2];
-    int shv[2], slv[2];
+    i32x8_t ah[2], al[2], bf[4];
+    int shv[2], slv[2], bsc[4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       ah[i] = p_frag(st, oa[i]);
@@ -410,17 +470,37 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const i32x8_t bfr = p_frag(st + 2 * P_TILE, ob[j]);
-      const int bsc = st[osb[j] + sb];
+      bf[j] = p_frag(st + 2 * P_TILE, ob[j]);
+      bsc[j] = st[osb[j] + sb];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (GRP == 0) p_lds_barrier();        // ends interval 2s
+    else if constexpr (DMA) p_wait8_barrier();      // ends interval 2s + 1
+    else p_wait0_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ah[i], bfr, acc[i][j], 0, 0, 0, shv[i], 0, bsc);
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al[i], bfr, acc[i][j], 0, 0, 0, slv[i], 0, bsc);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ah[i], bf[j], acc[i][j], 0, 0, 0, shv[i], 0, bsc[j]);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al[i], bf[j], acc[i][j], 0, 0, 0, slv[i], 0, bsc[j]);
       }
-    }
-    if (s + 2 < steps) p_wait8_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (GRP == 1) p_barrier_only();       // ends interval 2s + 2
+    else if constexpr (DMA) p_wait8_barrier();      // ends interval 2s + 1
     else p_wait0_barrier();
-  }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto pp_run = [&](auto grp_c) __attribute__((always_inline)) {
+    constexpr int GRP = decltype(grp_c)::value;
+    if constexpr (GRP == 1) p_barrier_only();  // group 1 starts one interval late
+    int s = 0;
+    for (; s + 2 < steps; ++s) pp_step(grp_c, std::true_type{}, s);
+    for (; s < steps; ++s) pp_step(grp_c, std::false_type{}, s);
+    if constexpr (GRP == 0) p_barrier_only();  // matches group 1's extra barrier
+  };
+  if (grp == 0) pp_run(std::integral_constant<int, 0>{});
+  else pp_run(std::integral_constant<int, 1>{});
 
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -435,8 +515,8 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
     }
 }
 
-// K % 128: whole step pairs, so every scale dword (4 bytes of a row) lies inside the
-// row and is 4-byte aligned; the DMA sources must be 16- / 4-byte aligned.
+// K % 128: whole step pairs (the tile-major scale layout); W rows must be 16-byte
+// aligned for the DMA, and the W scales 4-byte aligned for the repack.
 static bool gemm_mxfp8_pipe_ok(const QmmArgs &a) {
   return a.K % 128 == 0 && (uintptr_t)a.w % 16 == 0 && (uintptr_t)a.s % 4 == 0;
 }
@@ -445,23 +525,38 @@ bool gemm_mxfp8_ok(const QmmArgs &a) {
   return a.mode == MXFP8 && !a.x_f32 && a.K % F_BK == 0 && a.K > 0 && a.M > 0 && a.N > 0;
 }
 
+// Workspace: x hi, x lo (M x K bytes each), x hi / lo scales, and for the pipelined
+// kernel the W scales repacked, each scale array padded to whole 256-row tiles.
+static size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
+
 size_t gemm_mxfp8_workspace(const QmmArgs &a) {
-  const size_t mk = (size_t)a.M * a.K;
-  return 2 * mk + 2 * (mk / 32) + 256;
+  const size_t mk = round256(a.M) * a.K, nbk = (size_t)a.K / 32;
+  return 2 * mk + 2 * round256(a.M) * nbk + round256(a.N) * nbk + 256;
 }
 
 hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
   if (!gemm_mxfp8_ok(a)) return hipErrorInvalidValue;
-  const size_t mk = (size_t)a.M * a.K;
-  uint8_t *xh = (uint8_t *)ws, *xl = xh + mk, *sh = xl + mk, *sl = sh + mk / 32;
+  const size_t mk = round256(a.M) * a.K, nbk = (size_t)a.K / 32;
+  uint8_t *xh = (uint8_t *)ws, *xl = xh + mk, *sh = xl + mk, *sl = sh + round256(a.M) * nbk;
+  uint8_t *swp = sl + round256(a.M) * nbk;
+  const bool pipe = gemm_mxfp8_pipe_ok(a);
   const int64_t blocks_needed = ((int64_t)a.M * (a.K / 32) + 255) / 256;
   const int64_t sb = blocks_needed < 65536 ? blocks_needed : 65536;
-  hipLaunchKernelGGL(split_x_kernel, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (int64_t)a.M, a.K, xh, xl, sh,
-                     sl);
+  if (pipe)
+    hipLaunchKernelGGL(split_x_kernel<true>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (int64_t)a.M, a.K, xh,
+                       xl, sh, sl);
+  else
+    hipLaunchKernelGGL(split_x_kernel<false>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (int64_t)a.M, a.K, xh,
+                       xl, sh, sl);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int tiles = ((a.M + F_BM - 1) / F_BM) * ((a.N + F_BN - 1) / F_BN);
-  if (gemm_mxfp8_pipe_ok(a)) {
+  if (pipe) {
+    const int64_t dwords = (int64_t)round256(a.N) * (a.K / 128);
+    const int64_t rb = (dwords + 255) / 256 < 65536 ? (dwords + 255) / 256 : 65536;
+    hipLaunchKernelGGL(repack_scales_kernel, dim3(rb), dim3(256), 0, st, a.s, (int64_t)a.N, a.K, (uint32_t *)swp);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
     static bool pipe_attr_set = false;
     if (!pipe_attr_set) {
       e = hipFuncSetAttribute((const void *)gemm_mxfp8_pipe_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -469,7 +564,7 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
       if (e != hipSuccess) return e;
       pipe_attr_set = true;
     }
-    hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel, dim3(tiles), dim3(F_THREADS), P_LDS, st, xh, xl, sh, sl, a.w, a.s,
+    hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel, dim3(tiles), dim3(F_THREADS), P_LDS, st, xh, xl, sh, sl, a.w, swp,
                        (uint16_t *)a.y, a.M, a.N, a.K);
     return hipGetLastError();
   }
