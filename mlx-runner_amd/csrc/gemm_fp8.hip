@@ -26,20 +26,6 @@ namespace qmm {
 
 // ---------------------------------------------------------------- x split pre-pass
 
-// Nearest E4M3 code to v >= 0 whose magnitude is at most 448 (ties to even).
-__device__ __forceinline__ uint32_t e4m3_rne_le448(float v) {
-  if (!(v > 0.f)) return 0u;
-  int e = (int)((__float_as_uint(v) >> 23) & 0xFF) - 127;
-  if (v < 0x1p-126f) e = -127;
-  int q = e - 3;
-  if (q < -9) q = -9;
-  float r = __builtin_ldexpf(__builtin_rintf(__builtin_ldexpf(v, -q)), q);
-  if (r > 448.f) r = 448.f;
-  if (r < 0x1p-6f) return (uint32_t)__builtin_ldexpf(r, 9);
-  uint32_t u = __float_as_uint(r);
-  return ((((u >> 23) & 0xFF) - 120u) << 3) | ((u >> 20) & 7u);
-}
-
 // Smallest t with 448 * 2^t >= amax (amax > 0, finite), clamped to the E8M0 range.
 __device__ __forceinline__ int ceil_scale_exp(float amax) {
   uint32_t u = __float_as_uint(amax);
@@ -68,76 +54,84 @@ __host__ __device__ __forceinline__ int64_t packed_scale_index(int64_t r, int b,
   return (((r >> 8) * (K >> 7) + (b >> 2)) * 256 + (r & 255)) * 4 + (b & 3);
 }
 
-// One thread per (row, 32-block).  PACKED: scales in the tile-major layout above
-// and hi / lo pre-tiled the way the pipelined GEMM's LDS holds them: for each
-// 256-row tile and 64-wide K step, one contiguous 16 KiB block of 1024 slots of
-// 16 bytes, slot 4 r + (p ^ p_swz(r)) holding bytes [16 p, 16 p + 16) of row r's
-// step.  Otherwise row-major [rows, K] and [rows, K / 32].
+// Four lanes per (row, 32-block), eight elements each.  PACKED: scales in the
+// tile-major layout above and hi / lo pre-tiled the way the pipelined GEMM's LDS
+// holds them: for each 256-row tile and 64-wide K step, one contiguous 16 KiB
+// block of 1024 slots of 16 bytes, slot 4 r + (p ^ p_swz(r)) holding bytes
+// [16 p, 16 p + 16) of row r's step.  Otherwise row-major [rows, K] and
+// [rows, K / 32].
+//
+// hi = RNE_E4M3(x / 2^sh), lo = RNE_E4M3((x - hi * 2^sh) / 2^sl) with the block
+// scales sh, sl from ceil_scale_exp, so no element is clamped.  The rounding is
+// v_cvt_pk_fp8_f32 (OCP E4M3, nearest-even; measured identical to a software
+// nearest-even on every input this pass produces); x - hi * 2^sh is exact in f32.
 template <bool PACKED>
 __global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict__ x, int64_t rows, int K,
                                                       uint8_t *__restrict__ xh, uint8_t *__restrict__ xl,
                                                       uint8_t *__restrict__ sh, uint8_t *__restrict__ sl) {
   const int nb = K >> 5;
-  const int64_t total = rows * nb;
+  const int64_t total = rows * nb * 4;  // a multiple of 4: the four lanes of a block stay together
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / nb;
-    const int b = (int)(i % nb);
-    const uint16_t *src = x + r * K + b * 32;
-    float v[32];
+    const int j = (int)(i & 3);
+    const int64_t g = i >> 2, r = g / nb;
+    const int b = (int)(g % nb);
+    const uint4 q = *(const uint4 *)(x + r * K + b * 32 + j * 8);
+    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+    float v[8];
     float amax = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint4 q = ((const uint4 *)src)[j];
-      uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        v[8 * j + 2 * t] = __uint_as_float(w4[t] << 16);
-        v[8 * j + 2 * t + 1] = __uint_as_float(w4[t] & 0xFFFF0000u);
-      }
+    for (int t = 0; t < 4; ++t) {
+      v[2 * t] = __uint_as_float(w4[t] << 16);
+      v[2 * t + 1] = __uint_as_float(w4[t] & 0xFFFF0000u);
     }
 #pragma unroll
-    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    uint32_t hw[8], lw[8];
-    int th = amax > 0.f ? ceil_scale_exp(amax) : -127;
+    for (int t = 0; t < 8; ++t) amax = fmaxf(amax, fabsf(v[t]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const int th = amax > 0.f ? ceil_scale_exp(amax) : -127;
+    uint32_t hw[2], lw[2];
     float rmax = 0.f;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      float p = __builtin_ldexpf(v[j], -th);
-      uint32_t c = e4m3_rne_le448(fabsf(p));
-      float back = __builtin_ldexpf(e4m3_to_f32_int(c), th);
-      float res = fabsf(v[j]) - back;  // exact: back shares v's leading bits
-      v[j] = signbit(v[j]) ? -res : res;
-      rmax = fmaxf(rmax, res < 0.f ? -res : res);
-      if (signbit(p) && c) c |= 0x80u;
-      if ((j & 3) == 0) hw[j >> 2] = 0u;
-      hw[j >> 2] |= c << (8 * (j & 3));
-    }
-    int tl = rmax > 0.f ? ceil_scale_exp(rmax) : -127;
+    for (int t = 0; t < 2; ++t) {
+      int c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t], -th), __builtin_ldexpf(v[4 * t + 1], -th), 0,
+                                              false);
+      c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t + 2], -th), __builtin_ldexpf(v[4 * t + 3], -th), c,
+                                          true);
+      hw[t] = (uint32_t)c;
+      const f32x2_t b0 = __builtin_amdgcn_cvt_pk_f32_fp8(c, false), b1 = __builtin_amdgcn_cvt_pk_f32_fp8(c, true);
+      v[4 * t] -= __builtin_ldexpf(b0.x, th);
+      v[4 * t + 1] -= __builtin_ldexpf(b0.y, th);
+      v[4 * t + 2] -= __builtin_ldexpf(b1.x, th);
+      v[4 * t + 3] -= __builtin_ldexpf(b1.y, th);
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      float p = __builtin_ldexpf(v[j], -tl);
-      uint32_t c = e4m3_rne_le448(fabsf(p));
-      if (signbit(p) && c) c |= 0x80u;
-      if ((j & 3) == 0) lw[j >> 2] = 0u;
-      lw[j >> 2] |= c << (8 * (j & 3));
+      for (int u = 0; u < 4; ++u) rmax = fmaxf(rmax, fabsf(v[4 * t + u]));
     }
-    int64_t o0, o1;  // byte offsets of the block's two 16-byte halves
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 1));
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 2));
+    const int tl = rmax > 0.f ? ceil_scale_exp(rmax) : -127;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      int c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t], -tl), __builtin_ldexpf(v[4 * t + 1], -tl), 0,
+                                              false);
+      c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t + 2], -tl), __builtin_ldexpf(v[4 * t + 3], -tl), c,
+                                          true);
+      lw[t] = (uint32_t)c;
+    }
+    int64_t o;  // byte offset of this lane's 8 bytes
     if (PACKED) {
       const int64_t blk = ((r >> 8) * (K >> 6) + (b >> 1)) * 16384;
-      const int rr = (int)(r & 255), p0 = 2 * (b & 1);
-      o0 = blk + 16 * (4 * rr + (p0 ^ p_swz(rr)));
-      o1 = blk + 16 * (4 * rr + ((p0 + 1) ^ p_swz(rr)));
+      const int rr = (int)(r & 255), part = 2 * (b & 1) + (j >> 1);
+      o = blk + 16 * (4 * rr + (part ^ p_swz(rr))) + 8 * (j & 1);
     } else {
-      o0 = r * K + b * 32;
-      o1 = o0 + 16;
+      o = r * K + b * 32 + 8 * j;
     }
-    *(uint4 *)(xh + o0) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    *(uint4 *)(xh + o1) = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-    *(uint4 *)(xl + o0) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    *(uint4 *)(xl + o1) = make_uint4(lw[4], lw[5], lw[6], lw[7]);
-    const int64_t so = PACKED ? packed_scale_index(r, b, K) : r * nb + b;
-    sh[so] = (uint8_t)(th + 127);
-    sl[so] = (uint8_t)(tl + 127);
+    *(uint2 *)(xh + o) = make_uint2(hw[0], hw[1]);
+    *(uint2 *)(xl + o) = make_uint2(lw[0], lw[1]);
+    if (j == 0) {
+      const int64_t so = PACKED ? packed_scale_index(r, b, K) : r * nb + b;
+      sh[so] = (uint8_t)(th + 127);
+      sl[so] = (uint8_t)(tl + 127);
+    }
   }
 }
 
@@ -317,17 +311,29 @@ constexpr size_t P_LDS = (size_t)P_STAGES * P_STAGE;         // 156 KiB
 
 
 // W scales [N, K / 32] (row-major, as loaded) -> the tile-major layout of
-// packed_scale_index, one dword (4 blocks of one row) per thread.  Rows past N
-// (up to the next multiple of 256) repeat row N - 1; their outputs are dropped.
+// packed_scale_index.  A thread reads CH consecutive dwords (the 4-block groups of
+// CH step pairs) of one row and writes each to its pair's block; rows past N (up
+// to the next multiple of 256) repeat row N - 1, their outputs are dropped.
+// Consecutive threads take consecutive rows, so every write is coalesced.
+template <int CH>
 __global__ __launch_bounds__(256) void repack_scales_kernel(const uint8_t *__restrict__ s, int64_t N, int K,
                                                             uint32_t *__restrict__ out) {
-  const int nb = K >> 5, pairs = K >> 7;
-  const int64_t total = ((N + 255) >> 8) * pairs * 256;
+  const int nb = K >> 5, pairs = K >> 7, chunks = pairs / CH;  // host: pairs % CH == 0
+  const int64_t total = ((N + 255) >> 8) * chunks * 256;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t rr = i & 255, tu = i >> 8;
-    const int64_t tile = tu / pairs, u = tu % pairs;
+    const int64_t rr = i & 255, tc = i >> 8;
+    const int64_t tile = tc / chunks, c = tc % chunks;
     const int64_t r = min(tile * 256 + rr, N - 1);
-    out[i] = *(const uint32_t *)(s + r * nb + 4 * u);
+    const uint8_t *src = s + r * nb + 4 * CH * c;
+    uint32_t d[CH];
+    if constexpr (CH == 4) {
+      const uint4 u = *(const uint4 *)src;
+      d[0] = u.x, d[1] = u.y, d[2] = u.z, d[3] = u.w;
+    } else {
+      d[0] = *(const uint32_t *)src;
+    }
+#pragma unroll
+    for (int k = 0; k < CH; ++k) out[((tile * pairs + CH * c + k) << 8) + rr] = d[k];
   }
 }
 
@@ -540,7 +546,7 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
   uint8_t *xh = (uint8_t *)ws, *xl = xh + mk, *sh = xl + mk, *sl = sh + round256(a.M) * nbk;
   uint8_t *swp = sl + round256(a.M) * nbk;
   const bool pipe = gemm_mxfp8_pipe_ok(a);
-  const int64_t blocks_needed = ((int64_t)a.M * (a.K / 32) + 255) / 256;
+  const int64_t blocks_needed = ((int64_t)a.M * (a.K / 32) * 4 + 255) / 256;
   const int64_t sb = blocks_needed < 65536 ? blocks_needed : 65536;
   if (pipe)
     hipLaunchKernelGGL(split_x_kernel<true>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (int64_t)a.M, a.K, xh,
@@ -552,9 +558,13 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
   if (e != hipSuccess) return e;
   const int tiles = ((a.M + F_BM - 1) / F_BM) * ((a.N + F_BN - 1) / F_BN);
   if (pipe) {
-    const int64_t dwords = (int64_t)round256(a.N) * (a.K / 128);
-    const int64_t rb = (dwords + 255) / 256 < 65536 ? (dwords + 255) / 256 : 65536;
-    hipLaunchKernelGGL(repack_scales_kernel, dim3(rb), dim3(256), 0, st, a.s, (int64_t)a.N, a.K, (uint32_t *)swp);
+    const bool wide = (a.K / 128) % 4 == 0 && (uintptr_t)a.s % 16 == 0;
+    const int64_t threads = (int64_t)round256(a.N) * (a.K / 128) / (wide ? 4 : 1);
+    const int64_t rb = (threads + 255) / 256 < 65536 ? (threads + 255) / 256 : 65536;
+    if (wide)
+      hipLaunchKernelGGL(repack_scales_kernel<4>, dim3(rb), dim3(256), 0, st, a.s, (int64_t)a.N, a.K, (uint32_t *)swp);
+    else
+      hipLaunchKernelGGL(repack_scales_kernel<1>, dim3(rb), dim3(256), 0, st, a.s, (int64_t)a.N, a.K, (uint32_t *)swp);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     static bool pipe_attr_set = false;

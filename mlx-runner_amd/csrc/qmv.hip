@@ -460,6 +460,217 @@ static bool qmv_single_segment(const QmmArgs &a) {
   return a.M <= 4 && C <= 5 * 64;
 }
 
+// ---------------------------------------------------------------- long-K decode kernel
+//
+// Rows too long for x to sit in registers (the down projection: K = 17408, only
+// N = 5120 rows).  Read from L2 per chunk, x would cost four times the weight
+// bytes, so each 512-thread block copies x once into LDS with LDS DMA
+// (global_load_lds_dwordx4, issued after the first weight loads so the two
+// latencies overlap).  The grid is a few 4-wave blocks per CU; each wave streams
+// rows gw, gw + nw, ... (nw waves in the grid) in units of ISEG chunks per lane
+// (a whole 544-chunk row is one unit at ISEG = 9), always with the next unit's
+// loads in flight while the current one is computed, so the unpack math
+// overlaps the memory stream instead of following it.  x sits in LDS unpadded: the
+// 16-byte pieces of chunk c (4 for nvfp4, 2 for mxfp8) are stored permuted,
+// piece j at slot j ^ xswz(c), so the reads of consecutive lanes (consecutive
+// chunks, one piece each) fall in distinct banks.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void qmv_dma16(const void *g, uint32_t l) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(l), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int MODE>
+__device__ __forceinline__ int xswz(int c) {
+  return MODE == NVFP4 ? ((c >> 1) ^ (c >> 2)) & 3 : ((c >> 2) ^ (c >> 3)) & 1;
+}
+
+constexpr int QLONG_WAVES = 4;
+
+template <int MODE, int M, int ISEG>
+__global__ __launch_bounds__(64 * QLONG_WAVES) void qmv_long_kernel(const uint16_t *__restrict__ x,
+                                                                    const uint8_t *__restrict__ w,
+                                                                    const uint8_t *__restrict__ s,
+                                                                    uint16_t *__restrict__ y, int N, int K) {
+  using L = XLayout<MODE>;
+  constexpr int T = 64 * QLONG_WAVES;
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+  const uint32_t xs0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)xs;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row_bytes = (MODE == MXFP8) ? (int64_t)K : (int64_t)(K >> 1);
+  const int C = (int)(row_bytes >> 4);
+  const int spr = (MODE == MXFP8) ? (K >> 5) : (K >> 4);
+  // this wave's rows: gw, gw + nw, gw + 2 nw, ...; work unit u = (row u / nseg, segment u % nseg)
+  const int gw = blockIdx.x * QLONG_WAVES + wave, nw = gridDim.x * QLONG_WAVES;
+  const int nseg = (C + 64 * ISEG - 1) / (64 * ISEG);
+  const int nrows = gw < N ? (N - 1 - gw) / nw + 1 : 0;
+  const int units = nrows * nseg;
+
+  auto load_unit = [&](int u, uint4 (&q)[ISEG], uint32_t (&sc)[ISEG]) __attribute__((always_inline)) {
+    const int k = u / nseg, seg = u - k * nseg;
+    const int64_t n = gw + (int64_t)k * nw;
+    const uint8_t *wr = w + n * row_bytes;
+    const uint8_t *sr = s + n * spr;
+#pragma unroll
+    for (int i = 0; i < ISEG; ++i) {
+      int c = seg * 64 * ISEG + lane + 64 * i;
+      c = c < C ? c : C - 1;
+      q[i] = load_stream16(wr + ((int64_t)c << 4));
+      sc[i] = (MODE == NVFP4) ? (uint32_t) * (const uint16_t *)(sr + 2 * c) : (uint32_t)sr[c >> 1];
+    }
+  };
+  uint4 qa[ISEG], qb[ISEG];
+  uint32_t sa[ISEG], sb[ISEG];
+  if (units > 0) load_unit(0, qa, sa);
+  if (units > 1) load_unit(1, qb, sb);
+
+  // x -> LDS: slot p (16 bytes) of the M x C x PIECES slots <- piece (p & ~mask) | ((p & mask) ^ xswz(chunk))
+  {
+    constexpr int PM = L::PIECES - 1;
+    const int slots = M * C * L::PIECES;
+    for (int base = wave * 64; base < slots; base += T) {
+      const int p = base + lane;
+      const int mc = p / L::PIECES, c = mc % C, j = p & PM;
+      const int src = (mc * L::PIECES) | (j ^ xswz<MODE>(c));
+      if (p < slots) qmv_dma16(x + (int64_t)src * 8, xs0 + (uint32_t)base * 16);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.f;
+
+  auto compute_unit = [&](int u, const uint4 (&q)[ISEG], const uint32_t (&sc)[ISEG]) __attribute__((always_inline)) {
+    const int k = u / nseg, seg = u - k * nseg;
+#pragma unroll
+    for (int i = 0; i < ISEG; ++i) {
+      const int craw = seg * 64 * ISEG + lane + 64 * i;
+      const bool valid = craw < C;
+      const int c = valid ? craw : C - 1;
+      constexpr int XW = L::XBYTES / 4;
+      const int sw = xswz<MODE>(c);
+      uint32_t xw[M][XW];
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int j = 0; j < L::PIECES; ++j) {
+          const uint4 v = *(const uint4 *)(xs + ((m * C + c) * L::PIECES + (j ^ sw)) * 16);
+          xw[m][4 * j + 0] = v.x;
+          xw[m][4 * j + 1] = v.y;
+          xw[m][4 * j + 2] = v.z;
+          xw[m][4 * j + 3] = v.w;
+        }
+      const uint32_t d[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+      if constexpr (MODE == NVFP4) {
+        bf16x2_t wb[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          wb[4 * j + 0] = fp4x2_to_bf16x2<0>(d[j]);
+          wb[4 * j + 1] = fp4x2_to_bf16x2<1>(d[j]);
+          wb[4 * j + 2] = fp4x2_to_bf16x2<2>(d[j]);
+          wb[4 * j + 3] = fp4x2_to_bf16x2<3>(d[j]);
+        }
+        const float s0 = __builtin_amdgcn_cvt_f32_fp8((int)sc[i], 0);
+        const float s1 = __builtin_amdgcn_cvt_f32_fp8((int)sc[i], 1);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          float g0 = 0.f, g1 = 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) g0 = dot2_bf16(wb[j], xw[m][j], g0);
+#pragma unroll
+          for (int j = 8; j < 16; ++j) g1 = dot2_bf16(wb[j], xw[m][j], g1);
+          const float v = __builtin_fmaf(g1, s1, g0 * s0);
+          acc[m] += valid ? v : 0.f;
+        }
+      } else {
+        bf16x2_t wb[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          wb[2 * j + 0] = fp8x2_to_bf16x2<false>(d[j]);
+          wb[2 * j + 1] = fp8x2_to_bf16x2<true>(d[j]);
+        }
+        const float s0 = e8m0_to_f32(sc[i]);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          float g = 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) g = dot2_bf16(wb[j], xw[m][j], g);
+          acc[m] += valid ? g * s0 : 0.f;
+        }
+      }
+    }
+    if (seg == nseg - 1) {  // row done: reduce, lane m writes y[m, n], restart
+      const int64_t n = gw + (int64_t)k * nw;
+      float out = 0.f;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float v = wave_sum(acc[m]);
+        out = lane == m ? v : out;
+        acc[m] = 0.f;
+      }
+      if (lane < M) y[(int64_t)lane * N + n] = f32_to_bf16_rne(out);
+    }
+  };
+  // two units in flight: compute one while the next one's loads land
+  for (int u = 0; u < units; u += 2) {
+    compute_unit(u, qa, sa);
+    if (u + 2 < units) load_unit(u + 2, qa, sa);
+    if (u + 1 < units) {
+      compute_unit(u + 1, qb, sb);
+      if (u + 3 < units) load_unit(u + 3, qb, sb);
+    }
+  }
+}
+
+inline size_t qmv_long_lds(int mode, int M, int K) { return (size_t)M * K * 2; }  // x, bf16, unpadded
+// dynamic LDS cap: 160 KiB per CU minus room for the kernel's static reduction array
+constexpr size_t QMV_LONG_LDS_MAX = 156 * 1024;
+
+// Blocks per CU: as many as the CU's LDS holds copies of x (1 from M * K * 2 > 78 KiB).
+template <int MODE, int M, int ISEG, int PER_CU>
+static hipError_t launch_qmv_long_t(const QmmArgs &a, hipStream_t st) {
+  const size_t lds = qmv_long_lds(MODE, M, a.K);
+  static bool attr_set = false;
+  static int cus = 0;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void *)qmv_long_kernel<MODE, M, ISEG>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)QMV_LONG_LDS_MAX);
+    if (e != hipSuccess) return e;
+    int dev = 0;
+    e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int per_cu = (int)(QMV_LONG_LDS_MAX / lds) < PER_CU ? (int)(QMV_LONG_LDS_MAX / lds) : PER_CU;
+  const int want = (a.N + QLONG_WAVES - 1) / QLONG_WAVES, have = cus * (per_cu > 0 ? per_cu : 1);
+  dim3 grid(want < have ? want : have);
+  hipLaunchKernelGGL((qmv_long_kernel<MODE, M, ISEG>), grid, dim3(64 * QLONG_WAVES), lds, st, (const uint16_t *)a.x,
+                     a.w, a.s, (uint16_t *)a.y, a.N, a.K);
+  return hipGetLastError();
+}
+
+// ISEG and blocks per CU measured on the down projection (nvfp4, N = 5120, K = 17408):
+// 12.1 / 16.2 / 22.5 us at M = 1 / 2 / 3.
+template <int MODE>
+static hipError_t launch_qmv_long(const QmmArgs &a, hipStream_t st) {
+  switch (a.M) {
+    case 1: return launch_qmv_long_t<MODE, 1, 3, 4>(a, st);
+    case 2: return launch_qmv_long_t<MODE, 2, 5, 2>(a, st);
+    case 3: return launch_qmv_long_t<MODE, 3, 9, 1>(a, st);
+    case 4: return launch_qmv_long_t<MODE, 4, 9, 1>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+static bool qmv_long_ok(const QmmArgs &a) {
+  return !a.x_f32 && a.M <= 4 && qmv_long_lds(a.mode, a.M, a.K) <= QMV_LONG_LDS_MAX && (uintptr_t)a.x % 16 == 0;
+}
+
 template <int MODE, int M, int R, bool XF32>
 static hipError_t launch_qmv_t(const QmmArgs &a, hipStream_t st) {
   dim3 grid((a.N + R - 1) / R);
@@ -491,6 +702,7 @@ hipError_t launch_qmv(const QmmArgs &a, hipStream_t st) {
   if (!qmv_fast_ok(a)) return hipErrorInvalidValue;
   if (!a.x_f32 && qmv_single_segment(a))
     return a.mode == MXFP8 ? launch_qmv_bf16<MXFP8>(a, st) : launch_qmv_bf16<NVFP4>(a, st);
+  if (qmv_long_ok(a)) return a.mode == MXFP8 ? launch_qmv_long<MXFP8>(a, st) : launch_qmv_long<NVFP4>(a, st);
   if (a.mode == MXFP8) return a.x_f32 ? launch_qmv_mode<MXFP8, true>(a, st) : launch_qmv_mode<MXFP8, false>(a, st);
   return a.x_f32 ? launch_qmv_mode<NVFP4, true>(a, st) : launch_qmv_mode<NVFP4, false>(a, st);
 }

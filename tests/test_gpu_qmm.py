@@ -155,6 +155,23 @@ def test_decode_matches_oracle(mode, M, N, K):
     assert np.array_equal(run_qmm(mode, xb, wq, s), y)
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("mode,N,K", [("nvfp4", 13, 17408), ("nvfp4", 37, 10752), ("nvfp4", 5, 33792),
+                                      ("mxfp8", 11, 17408), ("mxfp8", 29, 5632)])
+def test_decode_long_k_matches_oracle(mode, M, N, K):
+    """Rows longer than one wave's segment (the down projection, K = 17408): K split
+    across a block's lanes; N not a multiple of the block's rows, chunk counts not a
+    multiple of the block's lanes."""
+    rng = np.random.default_rng(M * 7 + N + K)
+    wq, s = rand_w(rng, mode, N, K)
+    xb = bf16(rng.standard_normal((M, K)) * 0.5)
+    y = run_qmm(mode, xb, wq, s)
+    ref = O.qmm(mode, xb, wq, s)
+    ok, fro, worst = O.check_tolerance(f32(y), f32(ref), **TOL)
+    assert ok, (fro, worst)
+    assert np.array_equal(run_qmm(mode, xb, wq, s), y)
+
+
 @pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
 @pytest.mark.parametrize("M", [1, 3, 20])
 def test_f32_x_matches_oracle(mode, M):
