@@ -19,6 +19,7 @@
 // as 2 x 4 32x32 accumulators.
 #include <type_traits>
 
+#include "gemm_pipe.h"
 #include "qmm_device.h"
 #include "qmm_launch.h"
 
@@ -151,24 +152,6 @@ struct Fp8Smem {
   uint8_t s_lo[2][256 * 2];
   uint8_t s_b[2][256 * 2];
 };
-
-// Tile order: the hardware hands workgroup b to XCD b % 8.  Each XCD gets a
-// contiguous run of tile indices, and tiles are numbered in groups of 4 M-tiles
-// walked down M first, so the ~32 blocks resident on one XCD cover a 4 x 8
-// patch of (x rows, W rows) and share those operand slabs in that XCD's L2.
-__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int *tm, int *tn) {
-  const int T = tiles_m * tiles_n;
-  const int base = T / 8, rem = T % 8;
-  const int x = b % 8, local = b / 8;
-  const int t = x * base + (x < rem ? x : rem) + local;
-  constexpr int G = 4;
-  const int group = t / (G * tiles_n);
-  const int first_m = group * G;
-  const int gm = (tiles_m - first_m) < G ? (tiles_m - first_m) : G;
-  const int idx = t - group * G * tiles_n;
-  *tm = first_m + idx % gm;
-  *tn = idx / gm;
-}
 
 __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_kernel(
     const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
@@ -310,55 +293,6 @@ constexpr size_t P_LDS = (size_t)P_STAGES * P_STAGE;         // 156 KiB
 }  // namespace
 
 
-// W scales [N, K / 32] (row-major, as loaded) -> the tile-major layout of
-// packed_scale_index.  A thread reads CH consecutive dwords (the 4-block groups of
-// CH step pairs) of one row and writes each to its pair's block; rows past N (up
-// to the next multiple of 256) repeat row N - 1, their outputs are dropped.
-// Consecutive threads take consecutive rows, so every write is coalesced.
-template <int CH>
-__global__ __launch_bounds__(256) void repack_scales_kernel(const uint8_t *__restrict__ s, int64_t N, int K,
-                                                            uint32_t *__restrict__ out) {
-  const int nb = K >> 5, pairs = K >> 7, chunks = pairs / CH;  // host: pairs % CH == 0
-  const int64_t total = ((N + 255) >> 8) * chunks * 256;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t rr = i & 255, tc = i >> 8;
-    const int64_t tile = tc / chunks, c = tc % chunks;
-    const int64_t r = min(tile * 256 + rr, N - 1);
-    const uint8_t *src = s + r * nb + 4 * CH * c;
-    uint32_t d[CH];
-    if constexpr (CH == 4) {
-      const uint4 u = *(const uint4 *)src;
-      d[0] = u.x, d[1] = u.y, d[2] = u.z, d[3] = u.w;
-    } else {
-      d[0] = *(const uint32_t *)src;
-    }
-#pragma unroll
-    for (int k = 0; k < CH; ++k) out[((tile * pairs + CH * c + k) << 8) + rr] = d[k];
-  }
-}
-
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-// LDS DMA: lane i's 16 (4) bytes at g land at LDS byte l + 16 i (4 i); l must be wave-uniform.
-__device__ __forceinline__ void p_dma16(const void *g, uint32_t l) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(l), "v"(g) : "memory", "m0");
-}
-__device__ __forceinline__ void p_dma4(const void *g, uint32_t l) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(l), "v"(g) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-// Wait until this wave's DMAs of the next stage have landed (at most 8 of the
-// stage after it still in flight, or none) and its LDS reads of this stage are
-// done (the stage is refilled two steps later), then barrier the workgroup.
-__device__ __forceinline__ void p_wait8_barrier() {
-  asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-__device__ __forceinline__ void p_wait0_barrier() {
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-__device__ __forceinline__ void p_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-__device__ __forceinline__ void p_barrier_only() { asm volatile("s_barrier" ::: "memory"); }
-
 __device__ __forceinline__ i32x8_t p_frag(const uint8_t *base, int off) {
   const uint4 u0 = *(const uint4 *)(base + off), u1 = *(const uint4 *)(base + (off ^ 32));
   return i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
@@ -369,7 +303,7 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
     const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
     uint16_t *__restrict__ y, int M, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds;
+  const uint32_t lds0 = lds_addr(lds);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -406,15 +340,15 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
     const uint32_t st = lds0 + (uint32_t)((s % P_STAGES) * P_STAGE);
     const int k0 = s * P_BK;
     const int64_t xs = (int64_t)s * P_TILE;
-    p_dma16(ga_h[0] + xs, st + wave * 1024);
-    p_dma16(ga_h[1] + xs, st + (8 + wave) * 1024);
-    p_dma16(ga_l[0] + xs, st + P_TILE + wave * 1024);
-    p_dma16(ga_l[1] + xs, st + P_TILE + (8 + wave) * 1024);
-    p_dma16(gb[0] + k0, st + 2 * P_TILE + wave * 1024);
-    p_dma16(gb[1] + k0, st + 2 * P_TILE + (8 + wave) * 1024);
+    gp_dma16(ga_h[0] + xs, st + wave * 1024);
+    gp_dma16(ga_h[1] + xs, st + (8 + wave) * 1024);
+    gp_dma16(ga_l[0] + xs, st + P_TILE + wave * 1024);
+    gp_dma16(ga_l[1] + xs, st + P_TILE + (8 + wave) * 1024);
+    gp_dma16(gb[0] + k0, st + 2 * P_TILE + wave * 1024);
+    gp_dma16(gb[1] + k0, st + 2 * P_TILE + (8 + wave) * 1024);
     const int so = 1024 * (s >> 1);  // the step pair's 1 KiB block
-    p_dma4(gs[0] + so, st + 3 * P_TILE + (2 * wave) * 256);
-    p_dma4(gs[1] + so, st + 3 * P_TILE + (2 * wave + 1) * 256);
+    gp_dma4(gs[0] + so, st + 3 * P_TILE + (2 * wave) * 256);
+    gp_dma4(gs[1] + so, st + 3 * P_TILE + (2 * wave + 1) * 256);
   };
 
   // fragment geometry (32x32x64 operand layout: lane l holds row l % 32, K bytes 16 (l / 32) + [0, 16) and +32)
@@ -453,8 +387,8 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
   const int grp = wave >> 2;
   issue(0);
   if (steps > 1) issue(1);
-  if (steps > 1) p_wait8_barrier();
-  else p_wait0_barrier();
+  if (steps > 1) gp_wait_barrier<8>();
+  else gp_wait_barrier<0>();
 
   // one step of a group: loading interval (DMAs of step s + 2 if DMA, fragments of
   // step s), barrier, computing interval, barrier.  Each call is one basic block, so
@@ -480,9 +414,9 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
       bsc[j] = st[osb[j] + sb];
     }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (GRP == 0) p_lds_barrier();        // ends interval 2s
-    else if constexpr (DMA) p_wait8_barrier();      // ends interval 2s + 1
-    else p_wait0_barrier();
+    if constexpr (GRP == 0) gp_lds_barrier();        // ends interval 2s
+    else if constexpr (DMA) gp_wait_barrier<8>();      // ends interval 2s + 1
+    else gp_wait_barrier<0>();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -492,18 +426,18 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al[i], bf[j], acc[i][j], 0, 0, 0, slv[i], 0, bsc[j]);
       }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (GRP == 1) p_barrier_only();       // ends interval 2s + 2
-    else if constexpr (DMA) p_wait8_barrier();      // ends interval 2s + 1
-    else p_wait0_barrier();
+    if constexpr (GRP == 1) gp_barrier_only();       // ends interval 2s + 2
+    else if constexpr (DMA) gp_wait_barrier<8>();      // ends interval 2s + 1
+    else gp_wait_barrier<0>();
     __builtin_amdgcn_sched_barrier(0);
   };
   auto pp_run = [&](auto grp_c) __attribute__((always_inline)) {
     constexpr int GRP = decltype(grp_c)::value;
-    if constexpr (GRP == 1) p_barrier_only();  // group 1 starts one interval late
+    if constexpr (GRP == 1) gp_barrier_only();  // group 1 starts one interval late
     int s = 0;
     for (; s + 2 < steps; ++s) pp_step(grp_c, std::true_type{}, s);
     for (; s < steps; ++s) pp_step(grp_c, std::false_type{}, s);
-    if constexpr (GRP == 0) p_barrier_only();  // matches group 1's extra barrier
+    if constexpr (GRP == 0) gp_barrier_only();  // matches group 1's extra barrier
   };
   if (grp == 0) pp_run(std::integral_constant<int, 0>{});
   else pp_run(std::integral_constant<int, 1>{});
@@ -527,13 +461,26 @@ static bool gemm_mxfp8_pipe_ok(const QmmArgs &a) {
   return a.K % 128 == 0 && (uintptr_t)a.w % 16 == 0 && (uintptr_t)a.s % 4 == 0;
 }
 
+static size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+hipError_t launch_repack_scales(const uint8_t *s, int64_t N, int nb, uint32_t *out, hipStream_t st) {
+  const int dpr = nb / 4;
+  const bool wide = dpr % 4 == 0 && (uintptr_t)s % 16 == 0;
+  const int64_t threads = (int64_t)round256(N) * dpr / (wide ? 4 : 1);
+  const int64_t blocks = (threads + 255) / 256 < 65536 ? (threads + 255) / 256 : 65536;
+  if (wide)
+    hipLaunchKernelGGL(repack_scales_kernel<4>, dim3(blocks), dim3(256), 0, st, s, N, nb, out);
+  else
+    hipLaunchKernelGGL(repack_scales_kernel<1>, dim3(blocks), dim3(256), 0, st, s, N, nb, out);
+  return hipGetLastError();
+}
+
 bool gemm_mxfp8_ok(const QmmArgs &a) {
   return a.mode == MXFP8 && !a.x_f32 && a.K % F_BK == 0 && a.K > 0 && a.M > 0 && a.N > 0;
 }
 
 // Workspace: x hi, x lo (M x K bytes each), x hi / lo scales, and for the pipelined
 // kernel the W scales repacked, each scale array padded to whole 256-row tiles.
-static size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 size_t gemm_mxfp8_workspace(const QmmArgs &a) {
   const size_t mk = round256(a.M) * a.K, nbk = (size_t)a.K / 32;
@@ -558,14 +505,7 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
   if (e != hipSuccess) return e;
   const int tiles = ((a.M + F_BM - 1) / F_BM) * ((a.N + F_BN - 1) / F_BN);
   if (pipe) {
-    const bool wide = (a.K / 128) % 4 == 0 && (uintptr_t)a.s % 16 == 0;
-    const int64_t threads = (int64_t)round256(a.N) * (a.K / 128) / (wide ? 4 : 1);
-    const int64_t rb = (threads + 255) / 256 < 65536 ? (threads + 255) / 256 : 65536;
-    if (wide)
-      hipLaunchKernelGGL(repack_scales_kernel<4>, dim3(rb), dim3(256), 0, st, a.s, (int64_t)a.N, a.K, (uint32_t *)swp);
-    else
-      hipLaunchKernelGGL(repack_scales_kernel<1>, dim3(rb), dim3(256), 0, st, a.s, (int64_t)a.N, a.K, (uint32_t *)swp);
-    e = hipGetLastError();
+    e = launch_repack_scales(a.s, (int64_t)a.N, a.K / 32, (uint32_t *)swp, st);
     if (e != hipSuccess) return e;
     static bool pipe_attr_set = false;
     if (!pipe_attr_set) {

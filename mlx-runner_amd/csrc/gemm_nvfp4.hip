@@ -1,0 +1,236 @@
+// nvfp4 prefill GEMM on the bf16 MFMA (v_mfma_f32_32x32x16_bf16).
+//
+// y[M, N] = x[M, K] @ deq(W)[N, K].T, W in nvfp4 (E2M1 nibbles, one E4M3 scale
+// per 16), x bf16, fp32 accumulation, bf16 out.
+//
+// Why bf16 MFMA: an E2M1 value times an E4M3 scale has up to 5 significant bits,
+// which no 8-bit MFMA operand format holds, and the scaled MFMAs take only
+// E8M0 scales per 32; in bf16 (8 bits) the dequantized weight is exact.
+//
+// Same pipeline as the mxfp8 kernel: 256 x 256 block tile, K step 64, 8 waves
+// in two ping-pong groups, a 3-stage LDS ring filled by LDS DMA two steps ahead,
+// one barrier per interval.  Per stage:
+//   * x tile, 256 rows x 64 bf16 (128 bytes per row, moved in whole 128-byte
+//     row segments); 16-byte slot S of row r stored at slot S ^ aswz(r);
+//   * W tile kept in nvfp4, 256 rows x 32 bytes, moved by dword DMA and permuted
+//     so that a lane's four 8-element pieces (one per 16-wide K sub-step, the
+//     lane's half of it) are one 16-byte LDS read: dword (h, ks) of a row holds
+//     global dword 2 ks + h, the two 16-byte halves swapped by wswz(r);
+//   * the step's E4M3 scales, one dword (4 groups of 16) per W row, from the
+//     tile-major repacked copy.
+// Each wave owns 128 x 64 of the tile (4 x 2 accumulators).  The loading
+// interval reads the wave's W fragments and scales; the computing interval reads
+// x fragments per K sub-step and dequantizes W in registers (E2M1 -> f32, times
+// the scale, -> bf16: exact), interleaved with the MFMAs.
+#include <type_traits>
+
+#include "gemm_pipe.h"
+#include "qmm_device.h"
+#include "qmm_launch.h"
+
+namespace qmm {
+
+namespace {
+constexpr int V_BM = 256, V_BN = 256, V_BK = 64, V_THREADS = 512;
+constexpr int V_ATILE = 256 * 128;                 // x: 256 rows x 64 bf16
+constexpr int V_WTILE = 256 * 32;                  // W: 256 rows x 64 nvfp4
+constexpr int V_STILE = 2 * 1024;                  // scale dwords + 1 KiB spare
+constexpr int V_STAGE = V_ATILE + V_WTILE + V_STILE;  // 42 KiB
+constexpr int V_STAGES = 3;
+constexpr size_t V_LDS = (size_t)V_STAGES * V_STAGE;  // 126 KiB
+constexpr int V_DMA = 9;                              // DMAs per wave per step: 4 x, 4 W, 1 scale
+}  // namespace
+
+__device__ __forceinline__ int aswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int wswz(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
+
+// 8 nvfp4 elements (one dword, lowest nibble first) times the E4M3 scale byte, as 8 bf16.
+__device__ __forceinline__ bf16x8_t deq8_nvfp4(uint32_t word, uint32_t scale_byte) {
+  const float sc = __builtin_amdgcn_cvt_f32_fp8((int)scale_byte, 0);
+  bf16x8_t r;
+  const f32x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 0);
+  const f32x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 1);
+  const f32x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 2);
+  const f32x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 3);
+  r[0] = (__bf16)(p0.x * sc);
+  r[1] = (__bf16)(p0.y * sc);
+  r[2] = (__bf16)(p1.x * sc);
+  r[3] = (__bf16)(p1.y * sc);
+  r[4] = (__bf16)(p2.x * sc);
+  r[5] = (__bf16)(p2.y * sc);
+  r[6] = (__bf16)(p3.x * sc);
+  r[7] = (__bf16)(p3.y * sc);
+  return r;
+}
+
+__global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16_t *__restrict__ x,
+                                                                    const uint8_t *__restrict__ w,
+                                                                    const uint8_t *__restrict__ sp,
+                                                                    uint16_t *__restrict__ y, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const uint32_t lds0 = lds_addr(lds);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;  // wave tile: rows wm * 128 + [0, 128), cols wn * 64 + [0, 64)
+  int tm, tn;
+  tile_of(blockIdx.x, (M + V_BM - 1) / V_BM, (N + V_BN - 1) / V_BN, &tm, &tn);
+  const int m0 = tm * V_BM, n0 = tn * V_BN;
+  const int steps = K / V_BK;
+  const int64_t wrow = K >> 1;  // bytes per W row
+
+  // DMA sources (step 0).  x: wave-instruction g = wave + 8 i fills slots q = 64 g + lane.
+  const uint8_t *ga[4], *gw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int g = wave + 8 * i;
+    const int q = 64 * g + lane, row = q >> 3, part = (q & 7) ^ aswz(row);
+    ga[i] = (const uint8_t *)x + ((int64_t)min(m0 + row, M - 1) * K + part * 8) * 2;
+    // W: dword slot d = 64 g + lane of the tile: row d >> 3, physical half hp, sub-step ks
+    const int d = 64 * g + lane, wr = d >> 3, hp = (d >> 2) & 1, ks = d & 3, h = hp ^ wswz(wr);
+    gw[i] = w + (int64_t)min(n0 + wr, N - 1) * wrow + 4 * (2 * ks + h);
+  }
+  // scales: wave-instruction t = wave copies rows (t % 4) * 64 + lane of the step's 1 KiB block
+  // (t >= 4 re-read the same rows into the spare KiB)
+  const uint8_t *gs = sp + ((int64_t)tn * steps * 256 + (wave & 3) * 64 + lane) * 4;
+  auto issue = [&](int s) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + (uint32_t)((s % V_STAGES) * V_STAGE);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gp_dma16(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gp_dma4(gw[i] + s * 32, st + V_ATILE + (wave + 8 * i) * 256);
+    gp_dma4(gs + s * 1024, st + V_ATILE + V_WTILE + wave * 256);
+  };
+
+  // fragment geometry (32x32x16 bf16 operands: lane l holds row l % 32, K 8 (l / 32) + [0, 8) of the sub-step)
+  const int fr = lane & 31, fh = lane >> 5;
+  int oa[4], ab[4], ob[2], os[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = wm * 128 + i * 32 + fr;
+    oa[i] = r * 128;
+    ab[i] = fh ^ aswz(r);  // physical slot of logical slot 2 ks + fh is 2 ks ^ ab
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = wn * 64 + j * 32 + fr;
+    ob[j] = V_ATILE + r * 32 + 16 * (fh ^ wswz(r));
+    os[j] = V_ATILE + V_WTILE + r * 4;
+  }
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // Ping-pong (as in the mxfp8 kernel): group 0 (waves 0-3) loads step k's W
+  // fragments in interval 2k and computes in 2k + 1, group 1 (waves 4-7) one
+  // interval later; each SIMD holds one wave of each group.  Stage k is read up
+  // to interval 2k + 2 (group 1's computing interval reads x), so DMA(k + 2),
+  // which refills stage k - 1, is issued by both groups in interval 2k + 1
+  // (group 0 at the start of its computing interval, group 1 in its loading
+  // interval); at the barrier ending interval 2k + 1 every wave waits for its
+  // DMA(k + 1) (only DMA(k + 2), V_DMA loads, may remain in flight).
+  const int grp = wave >> 2;
+  issue(0);
+  if (steps > 1) issue(1);
+  if (steps > 1) gp_wait_barrier<V_DMA>();
+  else gp_wait_barrier<0>();
+
+  auto pp_step = [&](auto grp_c, auto dma_c, int s) __attribute__((always_inline)) {
+    constexpr int GRP = decltype(grp_c)::value;
+    constexpr bool DMA = decltype(dma_c)::value;
+    if constexpr (DMA && GRP == 1) issue(s + 2);  // interval 2s + 1
+    const uint8_t *st = lds + (s % V_STAGES) * V_STAGE;
+    uint4 wq[2];
+    uint32_t wsc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      wq[j] = *(const uint4 *)(st + ob[j]);
+      wsc[j] = *(const uint32_t *)(st + os[j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (GRP == 0) gp_lds_barrier();
+    else if constexpr (DMA) gp_wait_barrier<V_DMA>();
+    else gp_wait_barrier<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (DMA && GRP == 0) issue(s + 2);  // interval 2s + 1
+    // computing interval: x fragments are read per K sub-step, W fragments
+    // dequantized in place
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8_t af[4], bf[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = *(const bf16x8_t *)(st + oa[i] + 16 * ((2 * ks) ^ ab[i]));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t word = ks == 0 ? wq[j].x : ks == 1 ? wq[j].y : ks == 2 ? wq[j].z : wq[j].w;
+        bf[j] = deq8_nvfp4(word, (wsc[j] >> (8 * ks)) & 0xFF);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (GRP == 1) gp_lds_barrier();
+    else if constexpr (DMA) gp_wait_barrier<V_DMA>();
+    else gp_wait_barrier<0>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto pp_run = [&](auto grp_c) __attribute__((always_inline)) {
+    constexpr int GRP = decltype(grp_c)::value;
+    if constexpr (GRP == 1) gp_barrier_only();  // group 1 starts one interval late
+    int s = 0;
+    for (; s + 2 < steps; ++s) pp_step(grp_c, std::true_type{}, s);
+    for (; s < steps; ++s) pp_step(grp_c, std::false_type{}, s);
+    if constexpr (GRP == 0) gp_barrier_only();  // matches group 1's extra barrier
+  };
+  if (grp == 0) pp_run(std::integral_constant<int, 0>{});
+  else pp_run(std::integral_constant<int, 1>{});
+
+  // epilogue: 32x32 accumulator element v of lane l is row 8 (v / 4) + 4 (l / 32) + v % 4, col l % 32
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * 128 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (row < M && col < N) y[(int64_t)row * N + col] = f32_to_bf16_rne(acc[i][j][v]);
+      }
+    }
+}
+
+static size_t round256v(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// K % 64 (whole steps; the scale dword of a step is 4 groups); x rows 16-byte and
+// W rows / scale rows 4-byte aligned for the DMA and the repack.
+bool gemm_nvfp4_ok(const QmmArgs &a) {
+  return a.mode == NVFP4 && !a.x_f32 && a.K % V_BK == 0 && a.K > 0 && a.M > 0 && a.N > 0 &&
+         (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.w % 4 == 0 && (uintptr_t)a.s % 4 == 0;
+}
+
+size_t gemm_nvfp4_workspace(const QmmArgs &a) { return round256v(a.N) * (size_t)(a.K / 16) + 256; }
+
+hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
+  if (!gemm_nvfp4_ok(a)) return hipErrorInvalidValue;
+  hipError_t e = launch_repack_scales(a.s, (int64_t)a.N, a.K / 16, (uint32_t *)ws, st);
+  if (e != hipSuccess) return e;
+  static bool attr_set = false;
+  if (!attr_set) {
+    e = hipFuncSetAttribute((const void *)gemm_nvfp4_pipe_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)V_LDS);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int tiles = ((a.M + V_BM - 1) / V_BM) * ((a.N + V_BN - 1) / V_BN);
+  hipLaunchKernelGGL(gemm_nvfp4_pipe_kernel, dim3(tiles), dim3(V_THREADS), V_LDS, st, (const uint16_t *)a.x, a.w,
+                     (const uint8_t *)ws, (uint16_t *)a.y, a.M, a.N, a.K);
+  return hipGetLastError();
+}
+
+}  // namespace qmm

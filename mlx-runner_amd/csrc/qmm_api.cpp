@@ -485,6 +485,11 @@ int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array sca
     if (alloc_device(&ws, gemm_mxfp8_workspace(a), st)) return finish(1);
     e = launch_gemm_mxfp8(a, ws, st);
     (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
+  } else if (aligned && gemm_nvfp4_ok(a)) {
+    void *ws = nullptr;
+    if (alloc_device(&ws, gemm_nvfp4_workspace(a), st)) return finish(1);
+    e = launch_gemm_nvfp4(a, ws, st);
+    (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
   } else if (aligned && gemm_ok(a)) {
     e = launch_gemm(a, st);
   } else {

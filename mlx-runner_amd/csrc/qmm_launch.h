@@ -31,6 +31,9 @@ hipError_t launch_gemm(const QmmArgs &a, hipStream_t st);
 bool gemm_mxfp8_ok(const QmmArgs &a);
 size_t gemm_mxfp8_workspace(const QmmArgs &a);
 hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *workspace, hipStream_t st);
+bool gemm_nvfp4_ok(const QmmArgs &a);
+size_t gemm_nvfp4_workspace(const QmmArgs &a);
+hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *workspace, hipStream_t st);
 
 // dequant: out [N, K] float32 (out_f32) or bfloat16.
 hipError_t launch_dequant(int mode, const uint8_t *w, const uint8_t *s, int64_t N, int64_t K, void *out,
