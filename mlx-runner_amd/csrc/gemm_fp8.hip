@@ -269,125 +269,137 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_kernel(
 
 // ---------------------------------------------------------------- pipelined GEMM (K % 128 == 0)
 //
-// Same block tile (256 x 256, 8 waves of 64 x 128) and MFMA as above, with the
-// operand traffic moved off the VGPRs:
+// Same MFMA and wave layout as above (8 waves, 4 along x rows x 2 along W rows),
+// in two tile sizes: TS = 256 (waves of 64 x 128) for the bulk and TS = 128
+// (waves of 32 x 64) for a last partial round of the chip, split four ways so
+// that it takes a quarter of a round.  The operand traffic is off the VGPRs:
 //   * every operand byte goes global -> LDS directly (global_load_lds: lane i
 //     of a wave writes bytes [16 i, 16 i + 16) of the wave's 1 KiB destination,
 //     [4 i, 4 i + 4) for the dword form), into a 3-stage ring: the loads of step
-//     s + 2 are issued while step s computes, so a load has two steps (~2 x 2048
-//     MFMA cycles) to land;
+//     s + 2 are issued while step s computes;
 //   * the DMA is issued from inline assembly and waited for explicitly
 //     (s_waitcnt vmcnt), so no compiler-inserted wait serialises the ring;
-//   * a tile is 256 rows x 64 bytes, unpadded; 16-byte slot p of row r is stored
-//     at slot p ^ swz(r), swz(r) = ((r >> 1) ^ (r >> 2)) & 3, so the fragment
-//     reads of 8 (or 16) consecutive rows at one slot hit distinct banks;
+//   * an operand tile is TS rows x 64 bytes, unpadded; 16-byte slot p of row r is
+//     stored at slot p ^ p_swz(r), so the fragment reads of 8 (or 16) consecutive
+//     rows at one slot hit distinct banks; x hi / lo come pre-tiled in exactly
+//     this order (a 128-row tile is one half of a 256-row block), W row-major;
 //   * scales: per stage, the dword holding each row's 4 E8M0 bytes of the step
-//     pair (the step uses 2 of them) for x hi, x lo and W;
-//   * one barrier per step; each wave issues exactly 8 DMAs per step (6 tile,
-//     2 scale), the count the waits are written for.
+//     pair (the step uses 2 of them) for x hi, x lo and W, from the tile-major
+//     copies;
+//   * each wave issues exactly TS / 32 DMAs per step (3 TS / 128 tile, TS / 128
+//     scale), the count the waits are written for.
 namespace {
-constexpr int P_BK = 64, P_STAGES = 3, P_TILE = 256 * P_BK;  // 16 KiB per operand tile
-constexpr int P_SCALES = 4 * 1024;                           // x hi, x lo, W scale dwords + 1 KiB spare
-constexpr int P_STAGE = 3 * P_TILE + P_SCALES;               // 52 KiB
-constexpr size_t P_LDS = (size_t)P_STAGES * P_STAGE;         // 156 KiB
+constexpr int P_BK = 64, P_STAGES = 3;
+template <int TS>
+struct PipeGeom {
+  static constexpr int TILE = TS * P_BK;                  // one operand tile (bytes)
+  static constexpr int SCALES = 4 * TS * 4;               // x hi, x lo, W scale dwords + a spare block
+  static constexpr int STAGE = 3 * TILE + SCALES;         // 52 KiB at 256, 26 KiB at 128
+  static constexpr size_t LDS = (size_t)P_STAGES * STAGE;
+  static constexpr int TI = TS / 128;                     // tile DMAs per wave per operand
+  static constexpr int IPT = TS / 64;                     // scale DMAs per scale tensor
+  static constexpr int NDMA = 4 * TI;                     // DMAs per wave per step
+  static constexpr int FI = TS / 128, FJ = TS / 64;       // accumulators per wave
+};
 }  // namespace
-
 
 __device__ __forceinline__ i32x8_t p_frag(const uint8_t *base, int off) {
   const uint4 u0 = *(const uint4 *)(base + off), u1 = *(const uint4 *)(base + (off ^ 32));
   return i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
 }
 
+// Covers x rows [0, M) and W rows [n_begin, n_end) in TS x TS tiles.
+template <int TS>
 __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
     const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
     const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
-    uint16_t *__restrict__ y, int M, int N, int K) {
+    uint16_t *__restrict__ y, int M, int N, int K, int n_begin, int n_end) {
+  using G = PipeGeom<TS>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t lds0 = lds_addr(lds);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 1, wn = wave & 1;  // wave tile: rows wm * TS / 4 + [0, TS / 4), cols wn * TS / 2 + [0, TS / 2)
   int tm, tn;
-  tile_of(blockIdx.x, (M + F_BM - 1) / F_BM, (N + F_BN - 1) / F_BN, &tm, &tn);
-  const int m0 = tm * F_BM, n0 = tn * F_BN;
+  tile_of(blockIdx.x, (M + TS - 1) / TS, (n_end - n_begin + TS - 1) / TS, &tm, &tn);
+  const int m0 = tm * TS, n0 = n_begin + tn * TS;
   const int steps = K / P_BK;
 
-  // tile DMA: wave-instruction t (0, 1) of this wave fills LDS slots q = (8 t + wave) * 64 + lane
-  // (x hi / lo are pre-tiled: the tile's step block is contiguous, in LDS order;
-  // W is row-major: slot q holds row q >> 2, 16-byte part (q & 3) ^ swz(row))
-  const uint8_t *ga_h[2], *ga_l[2], *gb[2];
+  // tile DMA: wave-instruction t (< TI) of this wave fills LDS slots q = (8 t + wave) * 64 + lane
+  // (x hi / lo pre-tiled: a 256-row block's step is 1024 contiguous slots, rows m0 % 256 on;
+  // W row-major: slot q holds row q >> 2, 16-byte part (q & 3) ^ swz(row))
+  const uint8_t *ga_h[G::TI], *ga_l[G::TI], *gb[G::TI];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < G::TI; ++t) {
     const int q = (8 * t + wave) * 64 + lane, row = q >> 2, part = (q & 3) ^ p_swz(row);
-    const int64_t xo = (int64_t)tm * steps * P_TILE + q * 16;
+    const int64_t xo = (int64_t)(m0 >> 8) * steps * 16384 + ((m0 & 255) * 4 + q) * 16;
     ga_h[t] = xh + xo;
     ga_l[t] = xl + xo;
     gb[t] = w + (int64_t)min(n0 + row, N - 1) * K + part * 16;
   }
-  // scale DMA: wave-instruction t = 2 wave + {0, 1} of 16 copies the 256 contiguous
-  // bytes [(t % 4) * 256, + 256) of the step pair's 1 KiB block of tensor t / 4 (x hi,
-  // x lo, W, all tile-major; the 4th re-reads x hi into the spare KiB)
-  const uint8_t *gs[2];
+  // scale DMA: wave-instruction t = TI wave + h (h < TI) copies rows (t % IPT) * 64 + lane
+  // of tensor t / IPT (x hi, x lo, W, all tile-major; the 4th re-reads x hi into the spare block)
+  const uint8_t *gs[G::TI];
   const int pairs = K >> 7;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int t = 2 * wave + h, tensor = t >> 2, row = (t & 3) * 64 + lane;
+  for (int h = 0; h < G::TI; ++h) {
+    const int t = G::TI * wave + h, tensor = t / G::IPT, row = (t % G::IPT) * 64 + lane;
     const uint8_t *src = tensor == 1 ? sl : tensor == 2 ? sw : sh;
-    const int tile = tensor == 2 ? tn : tm;
-    gs[h] = src + ((int64_t)tile * pairs * 256 + row) * 4;
+    const int base = tensor == 2 ? n0 : m0;
+    gs[h] = src + ((int64_t)(base >> 8) * pairs * 256 + (base & 255) + row) * 4;
   }
   auto issue = [&](int s) __attribute__((always_inline)) {
-    const uint32_t st = lds0 + (uint32_t)((s % P_STAGES) * P_STAGE);
+    const uint32_t st = lds0 + (uint32_t)((s % P_STAGES) * G::STAGE);
     const int k0 = s * P_BK;
-    const int64_t xs = (int64_t)s * P_TILE;
-    gp_dma16(ga_h[0] + xs, st + wave * 1024);
-    gp_dma16(ga_h[1] + xs, st + (8 + wave) * 1024);
-    gp_dma16(ga_l[0] + xs, st + P_TILE + wave * 1024);
-    gp_dma16(ga_l[1] + xs, st + P_TILE + (8 + wave) * 1024);
-    gp_dma16(gb[0] + k0, st + 2 * P_TILE + wave * 1024);
-    gp_dma16(gb[1] + k0, st + 2 * P_TILE + (8 + wave) * 1024);
-    const int so = 1024 * (s >> 1);  // the step pair's 1 KiB block
-    gp_dma4(gs[0] + so, st + 3 * P_TILE + (2 * wave) * 256);
-    gp_dma4(gs[1] + so, st + 3 * P_TILE + (2 * wave + 1) * 256);
+    const int64_t xs = (int64_t)s * 16384;
+#pragma unroll
+    for (int t = 0; t < G::TI; ++t) {
+      gp_dma16(ga_h[t] + xs, st + (8 * t + wave) * 1024);
+      gp_dma16(ga_l[t] + xs, st + G::TILE + (8 * t + wave) * 1024);
+      gp_dma16(gb[t] + k0, st + 2 * G::TILE + (8 * t + wave) * 1024);
+    }
+    const int so = 1024 * (s >> 1);  // the step pair's block
+#pragma unroll
+    for (int h = 0; h < G::TI; ++h) gp_dma4(gs[h] + so, st + 3 * G::TILE + (G::TI * wave + h) * 256);
   };
 
   // fragment geometry (32x32x64 operand layout: lane l holds row l % 32, K bytes 16 (l / 32) + [0, 16) and +32)
   const int fr = lane & 31, fh = lane >> 5;
-  int oa[2], ob[4], osa[2], osb[4];
+  int oa[G::FI], ob[G::FJ], osa[G::FI], osb[G::FJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = wm * 64 + i * 32 + fr;
+  for (int i = 0; i < G::FI; ++i) {
+    const int r = wm * (TS / 4) + i * 32 + fr;
     oa[i] = r * P_BK + 16 * (fh ^ p_swz(r));
-    osa[i] = 3 * P_TILE + r * 4 + fh;
+    osa[i] = 3 * G::TILE + r * 4 + fh;
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = wn * 128 + j * 32 + fr;
+  for (int j = 0; j < G::FJ; ++j) {
+    const int r = wn * (TS / 2) + j * 32 + fr;
     ob[j] = r * P_BK + 16 * (fh ^ p_swz(r));
-    osb[j] = 3 * P_TILE + 2 * 1024 + r * 4 + fh;
+    osb[j] = 3 * G::TILE + 2 * TS * 4 + r * 4 + fh;
   }
 
-  f32x16_t acc[2][4];
+  f32x16_t acc[G::FI][G::FJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < G::FI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < G::FJ; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   // Ping-pong: waves 0-3 (group 0) and 4-7 (group 1) put one wave of each group on
-  // every SIMD.  Barrier intervals alternate: in each, one group runs the 16 MFMAs
+  // every SIMD.  Barrier intervals alternate: in each, one group runs the MFMAs
   // of its step while the other issues its DMAs and reads its next fragments, so
   // the MFMA pipe of every SIMD always has a wave feeding it.  Group 0 computes
   // step k in interval 2k + 1, group 1 in 2k + 2.  DMA(k + 2) overwrites the
   // stage group 1 read in interval 2k - 1, and is issued in the loading interval
   // of step k (2k, 2k + 1); at the barrier that ends interval 2k + 1 every wave
-  // waits for its DMA(k + 1) (only DMA(k + 2), 8 loads, may remain), so stage
+  // waits for its DMA(k + 1) (only DMA(k + 2), NDMA loads, may remain), so stage
   // k + 1 is whole before group 0 reads it in interval 2k + 2.
   const int grp = wave >> 2;
   issue(0);
   if (steps > 1) issue(1);
-  if (steps > 1) gp_wait_barrier<8>();
+  if (steps > 1) gp_wait_barrier<G::NDMA>();
   else gp_wait_barrier<0>();
 
   // one step of a group: loading interval (DMAs of step s + 2 if DMA, fragments of
@@ -397,37 +409,37 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
     constexpr int GRP = decltype(grp_c)::value;
     constexpr bool DMA = decltype(dma_c)::value;
     if constexpr (DMA) issue(s + 2);
-    const uint8_t *st = lds + (s % P_STAGES) * P_STAGE;
+    const uint8_t *st = lds + (s % P_STAGES) * G::STAGE;
     const int sb = 2 * (s & 1);  // byte of the pair dword: block fh of this step
-    i32x8_t ah[2], al[2], bf[4];
-    int shv[2], slv[2], bsc[4];
+    i32x8_t ah[G::FI], al[G::FI], bf[G::FJ];
+    int shv[G::FI], slv[G::FI], bsc[G::FJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < G::FI; ++i) {
       ah[i] = p_frag(st, oa[i]);
-      al[i] = p_frag(st + P_TILE, oa[i]);
+      al[i] = p_frag(st + G::TILE, oa[i]);
       shv[i] = st[osa[i] + sb];
-      slv[i] = st[osa[i] + 1024 + sb];
+      slv[i] = st[osa[i] + TS * 4 + sb];
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      bf[j] = p_frag(st + 2 * P_TILE, ob[j]);
+    for (int j = 0; j < G::FJ; ++j) {
+      bf[j] = p_frag(st + 2 * G::TILE, ob[j]);
       bsc[j] = st[osb[j] + sb];
     }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (GRP == 0) gp_lds_barrier();        // ends interval 2s
-    else if constexpr (DMA) gp_wait_barrier<8>();      // ends interval 2s + 1
+    if constexpr (GRP == 0) gp_lds_barrier();                // ends interval 2s
+    else if constexpr (DMA) gp_wait_barrier<G::NDMA>();      // ends interval 2s + 1
     else gp_wait_barrier<0>();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < G::FJ; ++j)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < G::FI; ++i) {
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ah[i], bf[j], acc[i][j], 0, 0, 0, shv[i], 0, bsc[j]);
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al[i], bf[j], acc[i][j], 0, 0, 0, slv[i], 0, bsc[j]);
       }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (GRP == 1) gp_barrier_only();       // ends interval 2s + 2
-    else if constexpr (DMA) gp_wait_barrier<8>();      // ends interval 2s + 1
+    if constexpr (GRP == 1) gp_barrier_only();               // ends interval 2s + 2
+    else if constexpr (DMA) gp_wait_barrier<G::NDMA>();      // ends interval 2s + 1
     else gp_wait_barrier<0>();
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -442,15 +454,16 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
   if (grp == 0) pp_run(std::integral_constant<int, 0>{});
   else pp_run(std::integral_constant<int, 1>{});
 
+  // epilogue: 32x32 accumulator element v of lane l is row 8 (v / 4) + 4 (l / 32) + v % 4, col l % 32
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < G::FI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = n0 + wn * 128 + j * 32 + (lane & 31);
+    for (int j = 0; j < G::FJ; ++j) {
+      const int col = n0 + wn * (TS / 2) + j * 32 + (lane & 31);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * 64 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (row < M && col < N) y[(int64_t)row * N + col] = f32_to_bf16_rne(acc[i][j][v]);
+        const int row = m0 + wm * (TS / 4) + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (row < M && col < n_end) y[(int64_t)row * N + col] = f32_to_bf16_rne(acc[i][j][v]);
       }
     }
 }
@@ -508,14 +521,38 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
     e = launch_repack_scales(a.s, (int64_t)a.N, a.K / 32, (uint32_t *)swp, st);
     if (e != hipSuccess) return e;
     static bool pipe_attr_set = false;
+    static int cus = 0;
     if (!pipe_attr_set) {
-      e = hipFuncSetAttribute((const void *)gemm_mxfp8_pipe_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)P_LDS);
+      e = hipFuncSetAttribute((const void *)gemm_mxfp8_pipe_kernel<256>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)PipeGeom<256>::LDS);
+      if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void *)gemm_mxfp8_pipe_kernel<128>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)PipeGeom<128>::LDS);
+      int dev = 0;
+      if (e == hipSuccess) e = hipGetDevice(&dev);
+      if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
       if (e != hipSuccess) return e;
       pipe_attr_set = true;
     }
-    hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel, dim3(tiles), dim3(F_THREADS), P_LDS, st, xh, xl, sh, sl, a.w, swp,
-                       (uint16_t *)a.y, a.M, a.N, a.K);
+    // One block per CU at a time (the ring fills most of a CU's LDS).  When the
+    // 256-tiles leave a last round that a whole number of W tile-columns fills
+    // and four times as many 128-tiles still fit one round, those columns run
+    // as 128-tiles: a quarter of the work per block, all in one round.
+    const int tiles_m = (a.M + 255) / 256, tiles_n = (a.N + 255) / 256;
+    const int rem = (tiles_m * tiles_n) % cus;
+    int n_split = a.N;
+    if (rem != 0 && rem % tiles_m == 0 && 4 * rem <= cus && tiles_m * tiles_n > cus) {
+      const int cols = rem / tiles_m;
+      n_split = (tiles_n - cols) * 256;
+    }
+    const int tiles1 = tiles_m * ((n_split + 255) / 256);
+    hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel<256>, dim3(tiles1), dim3(F_THREADS), PipeGeom<256>::LDS, st, xh, xl, sh,
+                       sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, 0, n_split);
+    e = hipGetLastError();
+    if (e != hipSuccess || n_split == a.N) return e;
+    const int tiles2 = ((a.M + 127) / 128) * ((a.N - n_split + 127) / 128);
+    hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel<128>, dim3(tiles2), dim3(F_THREADS), PipeGeom<128>::LDS, st, xh, xl, sh,
+                       sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, n_split, a.N);
     return hipGetLastError();
   }
   static bool attr_set = false;

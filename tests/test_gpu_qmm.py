@@ -172,6 +172,23 @@ def test_decode_long_k_matches_oracle(mode, M, N, K):
     assert np.array_equal(run_qmm(mode, xb, wq, s), y)
 
 
+def test_prefill_mxfp8_partial_last_round():
+    """x rows 300 (ragged against the 256-row tiles), W rows 33180: on a 256-CU
+    part the 256 x 256 tiles leave a last round of 4 tiles, which runs as 128 x 128
+    tiles over the last two tile-columns; every column from there on is checked
+    (plus a sample of the rest), all rows."""
+    mode, M, N, K = "mxfp8", 300, 33180, 256
+    rng = np.random.default_rng(11)
+    wq, s = rand_w(rng, mode, N, K)
+    xb = bf16(rng.standard_normal((M, K)))
+    y = run_qmm(mode, xb, wq, s)
+    cols = np.unique(np.concatenate([np.arange(32768 - 40, N), rng.choice(N, size=64, replace=False)]))
+    ref = O.qmm(mode, xb, wq, s, cols=cols)
+    ok, fro, worst = O.check_tolerance(f32(y[:, cols]), f32(ref), **TOL)
+    assert ok, (fro, worst)
+    assert np.array_equal(run_qmm(mode, xb, wq, s), y)
+
+
 @pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
 @pytest.mark.parametrize("M", [1, 3, 20])
 def test_f32_x_matches_oracle(mode, M):
