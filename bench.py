@@ -51,17 +51,20 @@ CONFIGS = {
                    workload="nvfp4 lm_head decode GEMV, x bf16 [1,5120], W [248320,5120]"),
     "lmhead_prefill": dict(mode="nvfp4", M=2048, N=248320, K=5120, xscale=1.0,
                            workload="nvfp4 lm_head prefill GEMM, x bf16 [2048,5120], W [248320,5120]"),
+    "dense_lmhead": dict(mode="bf16", M=1, N=248320, K=5120, xscale=1.0,
+                         workload="dense bf16 lm_head decode GEMV (mxfp8 checkpoints), x bf16 [1,5120], "
+                                  "W bf16 [248320,5120]"),
 }
 DEFAULT = "gateup"
-BITS = {"mxfp8": 8, "nvfp4": 4}
-GROUP = {"mxfp8": 32, "nvfp4": 16}
+BITS = {"mxfp8": 8, "nvfp4": 4, "bf16": 16}
+GROUP = {"mxfp8": 32, "nvfp4": 16, "bf16": None}
 ROTATE_BYTES = 512 << 20
 
 
 def algorithmic(cfg):
     M, N, K, mode = cfg["M"], cfg["N"], cfg["K"], cfg["mode"]
     wbytes = N * K * BITS[mode] // 8
-    sbytes = N * K // GROUP[mode]
+    sbytes = N * K // GROUP[mode] if GROUP[mode] else 0
     return dict(w=wbytes, s=sbytes, bytes=wbytes + sbytes + M * K * 2 + M * N * 2, flops=2 * M * N * K)
 
 
@@ -164,6 +167,9 @@ def main():
     for r in range(copies):
         gen.manual_seed(1000 + r)
         W = (torch.randn((N, K), generator=gen, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+        if mode == "bf16":
+            weights.append((Q.Array.from_torch(W), None))
+            continue
         wq, sc = Q.quantize(Q.Array.from_torch(W), mode, stream=stream)
         weights.append((wq, sc))
         del W
@@ -178,7 +184,10 @@ def main():
 
     def step(i, st):
         wq, sc = weights[i % copies]
-        Q.quantized_matmul(x, wq, sc, mode, out=y, stream=st)
+        if mode == "bf16":
+            Q.linear(x, wq, out=y, stream=st)
+        else:
+            Q.quantized_matmul(x, wq, sc, mode, out=y, stream=st)
 
     for i in range(args.warmup):
         step(i, stream)
@@ -230,7 +239,7 @@ def main():
     roof["traffic"] = traffic_from_profiles(args.config)
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and mode != "bf16":
         wq0, sc0 = weights[0]
         cpu = cpu_baseline(cfg, xt.view(torch.int16).cpu().numpy().view(np.uint16), wq0.numpy(), sc0.numpy())
 
@@ -239,7 +248,8 @@ def main():
     line = {
         "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 5), "us_per_call": round(ms * 1e3, 2), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": f"{mode} weights x bf16 (fp32 accumulate)",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 (fp32 accumulate)" if mode == "bf16" else f"{mode} weights x bf16 (fp32 accumulate)",
         "data": "synthetic (seeded N(0,1) x, N(0,0.02) W quantized on device)",
         "config": {"workload": cfg["workload"], "mode": mode, "M": M, "N": N, "K": K, "weight_copies": copies,
                    "algorithmic_bytes": alg["bytes"], "algorithmic_flops": alg["flops"],

@@ -295,8 +295,8 @@ def quantize(w: Array, mode: str, *, group_size=None, bits=None, stream: Stream 
     return outs[0], outs[1]
 
 
-def linear(x: Array, w: Array, *, stream: Stream | None = None) -> Array:
-    res = Array()
+def linear(x: Array, w: Array, *, out: Array | None = None, stream: Stream | None = None) -> Array:
+    res = out if out is not None else Array()
     s = _stream(stream)  # keep the wrapper alive across the call (its __del__ frees the handle)
     check(lib.qmm_linear(byref(res.h), x.h, w.h, s.h), "linear")
     return res

@@ -1,0 +1,108 @@
+"""The safetensors -> HBM loader and the named linear dispatch on the GPU.
+
+A small two-shard checkpoint (index json + shards, written here byte by byte in
+the safetensors format) holds quantized projections (U32 weights + U8 scales),
+a dense BF16 matrix and a norm vector.  The checks follow the reference's
+WeightMap.load (src/weights.zig:257-352) and namedLinearQ / linear
+(src/model.zig:200-233):
+  * tensors come back byte-identical in HBM, at their data_offsets;
+  * the quant spec is inferred from the shapes;
+  * named_linear_q on a packed weight equals the oracle's qmm of the same bytes,
+    and on a dense BF16 weight equals a float64 matmul;
+  * a name without ".weight", or a packed weight without scales, is MissingWeight.
+"""
+import json
+import struct
+
+import numpy as np
+import pytest
+
+import oracle as O
+import qmm as Q
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(rel_fro=1e-3, ulps=4.0)
+
+
+def bf16(a):
+    return O.f32_to_bf16_bits(np.asarray(a, np.float32))
+
+
+def write_safetensors(path, tensors):
+    """tensors: name -> (dtype string, numpy array of the raw element bytes)."""
+    header, blobs, off = {}, [], 0
+    for name, (dt, arr) in tensors.items():
+        raw = np.ascontiguousarray(arr).tobytes()
+        header[name] = {"dtype": dt, "shape": list(arr.shape), "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    h = json.dumps(header).encode()
+    h += b" " * ((8 - len(h) % 8) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def make_checkpoint(tmp_path, mode, N=48, K=256, V=40):
+    rng = np.random.default_rng(5 if mode == "mxfp8" else 6)
+    pre = "language_model.model.layers.0."
+    quant = {}
+    for proj in ("mlp.down_proj", "mlp.up_proj"):
+        W = O.bf16_bits_to_f32(bf16(rng.standard_normal((N, K)) * 0.02))
+        quant[proj] = O.quantize(mode, W)
+    dense = bf16(rng.standard_normal((V, K)) * 0.02)
+    norm = bf16(rng.standard_normal(K))
+    shard1 = {pre + "mlp.down_proj.weight": ("U32", quant["mlp.down_proj"][0]),
+              pre + "mlp.down_proj.scales": ("U8", quant["mlp.down_proj"][1]),
+              pre + "input_layernorm.weight": ("BF16", norm)}
+    shard2 = {pre + "mlp.up_proj.weight": ("U32", quant["mlp.up_proj"][0]),
+              pre + "mlp.up_proj.scales": ("U8", quant["mlp.up_proj"][1]),
+              "language_model.lm_head.weight": ("BF16", dense)}
+    write_safetensors(tmp_path / "model-00001-of-00002.safetensors", shard1)
+    write_safetensors(tmp_path / "model-00002-of-00002.safetensors", shard2)
+    wm = {k: "model-00001-of-00002.safetensors" for k in shard1}
+    wm.update({k: "model-00002-of-00002.safetensors" for k in shard2})
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": wm}))
+    return pre, quant, dense, norm
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+@pytest.mark.parametrize("M", [1, 3, 20])
+def test_loader_named_linear_q(tmp_path, mode, M):
+    N, K = 48, 256
+    pre, quant, dense, norm = make_checkpoint(tmp_path, mode, N=N, K=K)
+    wmap = Q.WeightMap(str(tmp_path))
+    assert len(wmap) == 6
+    assert wmap.quant == (mode, O.GROUP[mode], O.BITS[mode])
+    # bytes land unchanged
+    wq, s = quant["mlp.up_proj"]
+    assert np.array_equal(wmap.get(pre + "mlp.up_proj.weight").numpy(), wq)
+    assert np.array_equal(wmap.get(pre + "mlp.up_proj.scales").numpy(), s)
+    assert np.array_equal(wmap.get(pre + "input_layernorm.weight").numpy().view(np.uint16), norm)
+    rng = np.random.default_rng(M)
+    xb = bf16(rng.standard_normal((M, K)))
+    x = Q.Array.from_numpy(xb, Q.BFLOAT16)
+    for proj in ("mlp.down_proj", "mlp.up_proj"):
+        y = wmap.named_linear_q(x, pre + proj + ".weight").numpy()
+        ref = O.qmm(mode, xb, *quant[proj])
+        ok, fro, worst = O.check_tolerance(O.bf16_bits_to_f32(y), O.bf16_bits_to_f32(ref), **TOL)
+        assert ok, (proj, fro, worst)
+    # dense fallback: BF16 weight without scales
+    y = wmap.named_linear_q(x, "language_model.lm_head.weight").numpy()
+    ref = O.bf16_bits_to_f32(xb).astype(np.float64) @ O.bf16_bits_to_f32(dense).astype(np.float64).T
+    refb = np.array([[O.f64_to_bf16_bits(v) for v in r] for r in ref], np.uint16)
+    ok, fro, worst = O.check_tolerance(O.bf16_bits_to_f32(y), O.bf16_bits_to_f32(refb), **TOL)
+    assert ok, (fro, worst)
+
+
+def test_loader_missing_weight_errors(tmp_path):
+    pre, _, _, _ = make_checkpoint(tmp_path, "nvfp4")
+    wmap = Q.WeightMap(str(tmp_path))
+    x = Q.Array.from_numpy(bf16(np.ones((1, 256))), Q.BFLOAT16)
+    with pytest.raises(Q.QmmError, match="MissingWeight"):
+        wmap.named_linear_q(x, pre + "mlp.up_proj")  # no ".weight" suffix
+    with pytest.raises(Q.QmmError, match="MissingWeight"):
+        wmap.named_linear_q(x, pre + "mlp.gate_proj.weight")  # absent
