@@ -51,6 +51,9 @@ CONFIGS = {
                    workload="nvfp4 lm_head decode GEMV, x bf16 [1,5120], W [248320,5120]"),
     "lmhead_prefill": dict(mode="nvfp4", M=2048, N=248320, K=5120, xscale=1.0,
                            workload="nvfp4 lm_head prefill GEMM, x bf16 [2048,5120], W [248320,5120]"),
+    "mlp_gateup_silu": dict(mode="nvfp4", M=1, N=17408, K=5120, xscale=1.0, mlp=True,
+                            workload="nvfp4 MLP gate+up+SiLU*mul fused decode GEMV, x bf16 [1,5120], "
+                                     "W_gate, W_up [17408,5120]"),
     "dense_lmhead": dict(mode="bf16", M=1, N=248320, K=5120, xscale=1.0,
                          workload="dense bf16 lm_head decode GEMV (mxfp8 checkpoints), x bf16 [1,5120], "
                                   "W bf16 [248320,5120]"),
@@ -63,9 +66,10 @@ ROTATE_BYTES = 512 << 20
 
 def algorithmic(cfg):
     M, N, K, mode = cfg["M"], cfg["N"], cfg["K"], cfg["mode"]
-    wbytes = N * K * BITS[mode] // 8
-    sbytes = N * K // GROUP[mode] if GROUP[mode] else 0
-    return dict(w=wbytes, s=sbytes, bytes=wbytes + sbytes + M * K * 2 + M * N * 2, flops=2 * M * N * K)
+    mats = 2 if cfg.get("mlp") else 1  # the fused MLP reads a gate and an up matrix
+    wbytes = mats * N * K * BITS[mode] // 8
+    sbytes = mats * N * K // GROUP[mode] if GROUP[mode] else 0
+    return dict(w=wbytes, s=sbytes, bytes=wbytes + sbytes + M * K * 2 + M * N * 2, flops=2 * mats * M * N * K)
 
 
 def roofline_of(cfg, alg, sec_per_call):
@@ -171,6 +175,13 @@ def main():
             weights.append((Q.Array.from_torch(W), None))
             continue
         wq, sc = Q.quantize(Q.Array.from_torch(W), mode, stream=stream)
+        if cfg.get("mlp"):
+            gen.manual_seed(2000 + r)
+            W2 = (torch.randn((N, K), generator=gen, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+            wq2, sc2 = Q.quantize(Q.Array.from_torch(W2), mode, stream=stream)
+            weights.append((wq, sc, wq2, sc2))
+            del W, W2
+            continue
         weights.append((wq, sc))
         del W
     gen.manual_seed(7)
@@ -183,6 +194,10 @@ def main():
           f"warmup={args.warmup}", file=sys.stderr, flush=True)
 
     def step(i, st):
+        if cfg.get("mlp"):
+            wg, sg, wu, su = weights[i % copies]
+            Q.mlp_gate_up_silu(x, wg, sg, wu, su, mode, out=y, stream=st)
+            return
         wq, sc = weights[i % copies]
         if mode == "bf16":
             Q.linear(x, wq, out=y, stream=st)
@@ -239,7 +254,7 @@ def main():
     roof["traffic"] = traffic_from_profiles(args.config)
 
     cpu = None
-    if not args.no_cpu and mode != "bf16":
+    if not args.no_cpu and mode != "bf16" and not cfg.get("mlp"):
         wq0, sc0 = weights[0]
         cpu = cpu_baseline(cfg, xt.view(torch.int16).cpu().numpy().view(np.uint16), wq0.numpy(), sc0.numpy())
 

@@ -104,6 +104,20 @@ int qmm_dequantize(qmm_array *res, qmm_array w, qmm_array scales, qmm_array bias
 int qmm_quantize(qmm_vector_array *res, qmm_array w, qmm_optional_int group_size, qmm_optional_int bits,
                  const char *mode, qmm_array global_scale, qmm_stream s);
 
+/* silu(g) * u element-wise, with mlx-runner's per-op roundings in the arrays' dtype
+ * (bfloat16 or float32): sg = sigmoid(g), sl = g * sg, h = sl * u, each rounded
+ * (silu src/model.zig:405-415, mul :451-456).  g and u must have equal shapes. */
+int qmm_silu_mul(qmm_array *res, qmm_array g, qmm_array u, qmm_stream s);
+
+/* h = silu(x @ deq(Wg).T) * (x @ deq(Wu).T): the first three ops of mlpForwardQ
+ * (src/model.zig:905-913) in one call, same arguments as qmm_quantized_matmul for
+ * each projection.  Decode shapes (M <= 4) run one fused kernel (the gate and up
+ * rows of an output in one wave, the activation in its epilogue); the result
+ * equals quantized_matmul x 2 + silu_mul. */
+int qmm_mlp_gate_up_silu(qmm_array *res, qmm_array x, qmm_array w_gate, qmm_array s_gate, qmm_array w_up,
+                         qmm_array s_up, qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
+                         qmm_stream s);
+
 qmm_vector_array qmm_vector_array_new(void);
 int qmm_vector_array_free(qmm_vector_array v);
 size_t qmm_vector_array_size(qmm_vector_array v);
@@ -180,6 +194,10 @@ qmm_quant_spec qmm_weights_quant(qmm_weight_map m);
 int qmm_named_linear_q(qmm_array *res, qmm_weight_map m, qmm_array x, const char *name, qmm_stream s);
 /* Dense y = x @ w.T for bf16 x [..., M, K] and bf16 w [N, K] (linear, src/model.zig:200-211). */
 int qmm_linear(qmm_array *res, qmm_array x, qmm_array w, qmm_stream s);
+/* mlpForwardQ (src/model.zig:905-915): down(silu(gate(x)) * up(x)) by checkpoint
+ * names, in the reference's argument order (gate, down, up). */
+int qmm_mlp_forward_q(qmm_array *res, qmm_weight_map m, qmm_array x, const char *gate_name, const char *down_name,
+                      const char *up_name, qmm_stream s);
 
 /* Library / device info. */
 const char *qmm_version(void);

@@ -435,6 +435,44 @@ static int check_wq(const Arr *w, const Arr *sc, int mode, const char *op, int *
   return 0;
 }
 
+// y = x @ deq(W).T for the prepared arguments: picks the kernel family by shape.
+// Returns 0, or non-zero with the error latched.
+static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op) {
+  const int K = a.K, N = a.N;
+  const bool aligned = (((uintptr_t)a.x | (uintptr_t)a.w) & 15) == 0;
+  hipError_t e = hipSuccess;
+  if (K == 0) {
+    e = launch_fill_zero(a.y, ybytes, st);
+  } else if (a.M <= QMV_MAX_M) {
+    e = (aligned && qmv_fast_ok(a)) ? launch_qmv(a, st) : launch_qmv_generic(a, st);
+  } else if (aligned && gemm_mxfp8_ok(a)) {
+    void *ws = nullptr;
+    if (alloc_device(&ws, gemm_mxfp8_workspace(a), st)) return 1;
+    e = launch_gemm_mxfp8(a, ws, st);
+    (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
+  } else if (aligned && gemm_nvfp4_ok(a)) {
+    void *ws = nullptr;
+    if (alloc_device(&ws, gemm_nvfp4_workspace(a), st)) return 1;
+    e = launch_gemm_nvfp4(a, ws, st);
+    (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
+  } else if (aligned && gemm_ok(a)) {
+    e = launch_gemm(a, st);
+  } else {
+    // f32 x (or an unaligned view) with many rows: decode kernel over row blocks of 8.
+    const size_t esz = a.x_f32 ? 4 : 2;
+    for (int m0 = 0; m0 < a.M && e == hipSuccess; m0 += QMV_MAX_M) {
+      QmmArgs b = a;
+      b.M = a.M - m0 < QMV_MAX_M ? a.M - m0 : QMV_MAX_M;
+      b.x = (const char *)a.x + (size_t)m0 * K * esz;
+      b.y = (char *)a.y + (size_t)m0 * N * esz;
+      const bool al = (((uintptr_t)b.x | (uintptr_t)b.w) & 15) == 0;
+      e = (al && qmv_fast_ok(b)) ? launch_qmv(b, st) : launch_qmv_generic(b, st);
+    }
+  }
+  if (e != hipSuccess) return fail_hip(e, op);
+  return 0;
+}
+
 int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array scales, qmm_array biases,
                          bool transpose_w, qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
                          qmm_stream s) {
@@ -474,38 +512,97 @@ int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array sca
   a.w = (const uint8_t *)wa->data;
   a.s = (const uint8_t *)sa->data;
   a.y = ya->data;
-  const bool aligned = (((uintptr_t)a.x | (uintptr_t)a.w) & 15) == 0;
-  hipError_t e = hipSuccess;
-  if (K == 0) {
-    e = launch_fill_zero(a.y, ya->nbytes(), st);
-  } else if (a.M <= QMV_MAX_M) {
-    e = (aligned && qmv_fast_ok(a)) ? launch_qmv(a, st) : launch_qmv_generic(a, st);
-  } else if (aligned && gemm_mxfp8_ok(a)) {
-    void *ws = nullptr;
-    if (alloc_device(&ws, gemm_mxfp8_workspace(a), st)) return finish(1);
-    e = launch_gemm_mxfp8(a, ws, st);
-    (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
-  } else if (aligned && gemm_nvfp4_ok(a)) {
-    void *ws = nullptr;
-    if (alloc_device(&ws, gemm_nvfp4_workspace(a), st)) return finish(1);
-    e = launch_gemm_nvfp4(a, ws, st);
-    (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
-  } else if (aligned && gemm_ok(a)) {
-    e = launch_gemm(a, st);
-  } else {
-    // f32 x (or an unaligned view) with many rows: decode kernel over row blocks of 8.
-    const size_t esz = a.x_f32 ? 4 : 2;
-    for (int m0 = 0; m0 < a.M && e == hipSuccess; m0 += QMV_MAX_M) {
-      QmmArgs b = a;
-      b.M = a.M - m0 < QMV_MAX_M ? a.M - m0 : QMV_MAX_M;
-      b.x = (const char *)a.x + (size_t)m0 * K * esz;
-      b.y = (char *)a.y + (size_t)m0 * N * esz;
-      const bool al = (((uintptr_t)b.x | (uintptr_t)b.w) & 15) == 0;
-      e = (al && qmv_fast_ok(b)) ? launch_qmv(b, st) : launch_qmv_generic(b, st);
-    }
-  }
+  if (run_qmm(a, ya->nbytes(), st, op)) return finish(1);
+  return finish(0);
+}
+
+int qmm_silu_mul(qmm_array *res, qmm_array g, qmm_array u, qmm_stream s) {
+  const char *op = "silu_mul";
+  if (!res) return finish(fail("[%s] null result pointer", op));
+  Arr *ga = (Arr *)g.ctx, *ua = (Arr *)u.ctx;
+  if (!ga || !ua) return finish(fail("[%s] missing input", op));
+  if (ga->dtype != ua->dtype || (ga->dtype != QMM_BFLOAT16 && ga->dtype != QMM_FLOAT32))
+    return finish(fail("[%s] inputs must both be bfloat16 or both float32", op));
+  if (ga->ndim != ua->ndim) return finish(fail("[%s] shapes differ", op));
+  for (int i = 0; i < ga->ndim; ++i)
+    if (ga->shape[i] != ua->shape[i]) return finish(fail("[%s] shapes differ", op));
+  std::vector<int> shape(ga->shape, ga->shape + ga->ndim);
+  hipStream_t st = stream_of(s);
+  Arr *ha;
+  if (alloc_arr(res, shape, ga->dtype, st, &ha)) return finish(1);
+  const int64_t n = (int64_t)ga->size();
+  hipError_t e = launch_silu_mul(ga->data, ua->data, ha->data, n, ga->dtype == QMM_FLOAT32, st);
   if (e != hipSuccess) return finish(fail_hip(e, op));
   return finish(0);
+}
+
+int qmm_mlp_gate_up_silu(qmm_array *res, qmm_array x, qmm_array w_gate, qmm_array s_gate, qmm_array w_up,
+                         qmm_array s_up, qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
+                         qmm_stream s) {
+  const char *op = "mlp_gate_up_silu";
+  if (!res) return finish(fail("[%s] null result pointer", op));
+  int m;
+  if (parse_mode(mode, group_size, bits, op, &m)) return finish(1);
+  Arr *xa = (Arr *)x.ctx;
+  if (!xa) return finish(fail("[%s] missing x", op));
+  int N, K, N2, K2;
+  if (check_wq((Arr *)w_gate.ctx, (Arr *)s_gate.ctx, m, op, &N, &K)) return finish(1);
+  if (check_wq((Arr *)w_up.ctx, (Arr *)s_up.ctx, m, op, &N2, &K2)) return finish(1);
+  if (N != N2 || K != K2) return finish(fail("[%s] gate [%d, %d] and up [%d, %d] differ", op, N, K, N2, K2));
+  if (xa->dtype != QMM_BFLOAT16 && xa->dtype != QMM_FLOAT32)
+    return finish(fail("[%s] x must be bfloat16 or float32", op));
+  if (xa->ndim < 1 || xa->shape[xa->ndim - 1] != K)
+    return finish(fail("[%s] Last dimension of x does not match the weight's K (%d)", op, K));
+  int64_t M = 1;
+  for (int i = 0; i < xa->ndim - 1; ++i) M *= xa->shape[i];
+  if (M > INT32_MAX) return finish(fail("[%s] too many rows", op));
+  std::vector<int> oshape(xa->shape, xa->shape + xa->ndim);
+  oshape.back() = N;
+  hipStream_t st = stream_of(s);
+  Arr *ha;
+  if (alloc_arr(res, oshape, xa->dtype, st, &ha)) return finish(1);
+  if (M == 0 || N == 0) return finish(0);
+  QmmArgs a;
+  a.mode = m;
+  a.x_f32 = xa->dtype == QMM_FLOAT32;
+  a.M = (int)M;
+  a.N = N;
+  a.K = K;
+  a.x = xa->data;
+  a.w = (const uint8_t *)((Arr *)w_gate.ctx)->data;
+  a.s = (const uint8_t *)((Arr *)s_gate.ctx)->data;
+  a.y = ha->data;
+  const uint8_t *wu = (const uint8_t *)((Arr *)w_up.ctx)->data, *su = (const uint8_t *)((Arr *)s_up.ctx)->data;
+  if (K > 0 && qmv_mlp_ok(a) && ((uintptr_t)wu & 15) == 0) {
+    hipError_t e = launch_qmv_mlp(a, wu, su, st);
+    if (e != hipSuccess) return finish(fail_hip(e, op));
+    return finish(0);
+  }
+  // prefill shapes: the two projections, then the activation
+  const size_t bytes = ha->nbytes();
+  void *g = nullptr, *u = nullptr;
+  if (alloc_device(&g, bytes, st)) return finish(1);
+  if (alloc_device(&u, bytes, st)) {
+    (void)hipFreeAsync(g, st);
+    return finish(1);
+  }
+  int rc = 0;
+  a.y = g;
+  rc = run_qmm(a, bytes, st, op);
+  if (!rc) {
+    QmmArgs b = a;
+    b.w = wu;
+    b.s = su;
+    b.y = u;
+    rc = run_qmm(b, bytes, st, op);
+  }
+  if (!rc) {
+    hipError_t e = launch_silu_mul(g, u, ha->data, (int64_t)M * N, a.x_f32, st);
+    if (e != hipSuccess) rc = fail_hip(e, op);
+  }
+  (void)hipFreeAsync(g, st);
+  (void)hipFreeAsync(u, st);
+  return finish(rc ? 1 : 0);
 }
 
 int qmm_dequantize(qmm_array *res, qmm_array w, qmm_array scales, qmm_array biases, qmm_optional_int group_size,

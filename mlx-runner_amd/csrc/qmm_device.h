@@ -99,6 +99,19 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
+
+// mlx-runner's MLP activation on bf16 arrays (src/model.zig:405-415 silu, :451-456
+// mul, used by mlpForwardQ :905-915), every op rounding its result to bf16:
+//   g, u = the two projections (bf16), sg = sigmoid(g), sl = g * sg, h = sl * u.
+// sigmoid is 1 / (1 + exp(-g)) in f32.  Returns h in f32, already a bf16 value.
+__device__ __forceinline__ float silu_mul_bf16(float g, float u) {
+  const float gb = bf16_round(g), ub = bf16_round(u);
+  const float sg = bf16_round(1.f / (1.f + expf(-gb)));
+  const float sl = bf16_round(gb * sg);
+  return bf16_round(sl * ub);
+}
+
 // Sum over the 64 lanes of a wave; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -234,18 +234,23 @@ inline size_t qmv_lds_bytes(int mode, int M, int K) {
 }
 constexpr size_t QMV_LDS_MAX = 64 * 1024;
 
-template <int MODE, int M, int R, int ISEG, int XP, bool DB>
+// MLP: the wave's two rows are row n of W (gate) and row n of W2 (up), and the
+// output is silu(gate) * up with the reference's bf16 roundings (silu_mul_bf16).
+template <int MODE, int M, int R, int ISEG, int XP, bool DB, bool MLP = false>
 __global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t *__restrict__ x,
                                                                   const uint8_t *__restrict__ w,
                                                                   const uint8_t *__restrict__ s,
-                                                                  uint16_t *__restrict__ y, int N, int K) {
+                                                                  uint16_t *__restrict__ y, int N, int K,
+                                                                  const uint8_t *__restrict__ w2 = nullptr,
+                                                                  const uint8_t *__restrict__ s2 = nullptr) {
   using L = XLayout<MODE>;
   constexpr int THREADS = 64 * QMV_WAVES;
   constexpr bool XLDS = XP > 0;  // XP: x pieces staged per thread (2 or 4; 0: x read from global)
   static_assert(XP == 0 || XP == 2 || XP == 4, "x staging supports 2 or 4 pieces per thread");
+  static_assert(!MLP || R == 2, "the MLP form pairs one gate row with one up row");
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n0 = (blockIdx.x * QMV_WAVES + wave) * R;
+  const int n0 = (blockIdx.x * QMV_WAVES + wave) * (MLP ? 1 : R);
   const int64_t row_bytes = (MODE == MXFP8) ? (int64_t)K : (int64_t)(K >> 1);
   const int C = (int)(row_bytes >> 4);
   const int spr = (MODE == MXFP8) ? (K >> 5) : (K >> 4);
@@ -253,9 +258,15 @@ __global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t
   const uint8_t *srow[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int n = n0 + r < N ? n0 + r : N - 1;  // tail rows re-read row N-1; results dropped
-    wrow[r] = w + (int64_t)n * row_bytes;
-    srow[r] = s + (int64_t)n * spr;
+    if constexpr (MLP) {
+      const int n = n0 < N ? n0 : N - 1;
+      wrow[r] = (r == 0 ? w : w2) + (int64_t)n * row_bytes;
+      srow[r] = (r == 0 ? s : s2) + (int64_t)n * spr;
+    } else {
+      const int n = n0 + r < N ? n0 + r : N - 1;  // tail rows re-read row N-1; results dropped
+      wrow[r] = w + (int64_t)n * row_bytes;
+      srow[r] = s + (int64_t)n * spr;
+    }
   }
 
   // 1) x staging loads first: the LDS write below then waits only for these,
@@ -401,6 +412,16 @@ __global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t
     }
   }
 
+  if constexpr (MLP) {
+    float out = 0.f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float g = wave_sum(acc[0][m]), u = wave_sum(acc[1][m]);
+      out = (lane == m) ? silu_mul_bf16(g, u) : out;
+    }
+    if (lane < M && n0 < N) y[(int64_t)lane * N + n0] = f32_to_bf16_rne(out);
+    return;
+  }
   float out = 0.f;
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -453,6 +474,31 @@ static hipError_t launch_qmv_bf16(const QmmArgs &a, hipStream_t st) {
     case 4: return launch_qmv_bf16_m<MODE, 4>(a, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+template <int MODE, int M>
+static hipError_t launch_qmv_mlp_m(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st) {
+  const int C = MODE == MXFP8 ? a.K / 16 : a.K / 32;
+  const size_t lds = qmv_lds_bytes(MODE, M, a.K);
+  const int pieces = M * C * (MODE == NVFP4 ? 4 : 2);
+  constexpr int T = 64 * QMV_WAVES;
+  dim3 grid((a.N + QMV_WAVES - 1) / QMV_WAVES);
+  const uint16_t *x = (const uint16_t *)a.x;
+  uint16_t *y = (uint16_t *)a.y;
+#define QMV_MLP_LAUNCH(IS, XP)                                                                                 \
+  hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, 2, IS, XP, false, true>), grid, dim3(T), XP ? lds : 0, st, x, a.w, \
+                     a.s, y, a.N, a.K, w_up, s_up)
+  if (C <= 3 * 64) {
+    if (lds <= QMV_LDS_MAX && pieces <= 2 * T) QMV_MLP_LAUNCH(3, 2);
+    else if (lds <= QMV_LDS_MAX && pieces <= 4 * T) QMV_MLP_LAUNCH(3, 4);
+    else QMV_MLP_LAUNCH(3, 0);
+  } else {
+    if (lds <= QMV_LDS_MAX && pieces <= 2 * T) QMV_MLP_LAUNCH(5, 2);
+    else if (lds <= QMV_LDS_MAX && pieces <= 4 * T) QMV_MLP_LAUNCH(5, 4);
+    else QMV_MLP_LAUNCH(5, 0);
+  }
+#undef QMV_MLP_LAUNCH
+  return hipGetLastError();
 }
 
 static bool qmv_single_segment(const QmmArgs &a) {
@@ -705,6 +751,50 @@ hipError_t launch_qmv(const QmmArgs &a, hipStream_t st) {
   if (qmv_long_ok(a)) return a.mode == MXFP8 ? launch_qmv_long<MXFP8>(a, st) : launch_qmv_long<NVFP4>(a, st);
   if (a.mode == MXFP8) return a.x_f32 ? launch_qmv_mode<MXFP8, true>(a, st) : launch_qmv_mode<MXFP8, false>(a, st);
   return a.x_f32 ? launch_qmv_mode<NVFP4, true>(a, st) : launch_qmv_mode<NVFP4, false>(a, st);
+}
+
+bool qmv_mlp_ok(const QmmArgs &a) {
+  return !a.x_f32 && a.M >= 1 && a.M <= 4 && qmv_fast_ok(a) && qmv_single_segment(a) &&
+         (((uintptr_t)a.x | (uintptr_t)a.w) & 15) == 0;
+}
+
+hipError_t launch_qmv_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st) {
+  if (!qmv_mlp_ok(a) || ((uintptr_t)w_up & 15) != 0) return hipErrorInvalidValue;
+  const bool mx = a.mode == MXFP8;
+  switch (a.M) {
+    case 1: return mx ? launch_qmv_mlp_m<MXFP8, 1>(a, w_up, s_up, st) : launch_qmv_mlp_m<NVFP4, 1>(a, w_up, s_up, st);
+    case 2: return mx ? launch_qmv_mlp_m<MXFP8, 2>(a, w_up, s_up, st) : launch_qmv_mlp_m<NVFP4, 2>(a, w_up, s_up, st);
+    case 3: return mx ? launch_qmv_mlp_m<MXFP8, 3>(a, w_up, s_up, st) : launch_qmv_mlp_m<NVFP4, 3>(a, w_up, s_up, st);
+    default: return mx ? launch_qmv_mlp_m<MXFP8, 4>(a, w_up, s_up, st) : launch_qmv_mlp_m<NVFP4, 4>(a, w_up, s_up, st);
+  }
+}
+
+// ---------------------------------------------------------------- silu(g) * u, element-wise
+
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const T *__restrict__ g, const T *__restrict__ u,
+                                                       T *__restrict__ h, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    if constexpr (sizeof(T) == 2) {
+      h[i] = f32_to_bf16_rne(silu_mul_bf16(bf16_to_f32(g[i]), bf16_to_f32(u[i])));
+    } else {
+      const float gv = g[i];
+      const float sg = 1.f / (1.f + expf(-gv));
+      h[i] = (gv * sg) * u[i];
+    }
+  }
+}
+
+hipError_t launch_silu_mul(const void *g, const void *u, void *h, int64_t n, bool f32, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = (n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536;
+  if (f32)
+    hipLaunchKernelGGL(silu_mul_kernel<float>, dim3(blocks), dim3(256), 0, st, (const float *)g, (const float *)u,
+                       (float *)h, n);
+  else
+    hipLaunchKernelGGL(silu_mul_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, (const uint16_t *)g,
+                       (const uint16_t *)u, (uint16_t *)h, n);
+  return hipGetLastError();
 }
 
 hipError_t launch_qmv_generic(const QmmArgs &a, hipStream_t st) {

@@ -599,4 +599,39 @@ int qmm_named_linear_q(qmm_array *res, qmm_weight_map m, qmm_array x, const char
                               qmm_optional_int{(int)wm->quant.bits, true}, mode, s);
 }
 
+// mlpForwardQ (src/model.zig:905-915): down(silu(gate(x)) * up(x)), the projections
+// named as in the checkpoint ("....mlp.gate_proj.weight" etc.).  When gate and up
+// are packed with scales the first three ops run fused (qmm_mlp_gate_up_silu);
+// otherwise each goes through named_linear_q and the activation is qmm_silu_mul.
+int qmm_mlp_forward_q(qmm_array *res, qmm_weight_map m, qmm_array x, const char *gate_name, const char *down_name,
+                      const char *up_name, qmm_stream s) {
+  WeightMap *wm = (WeightMap *)m.ctx;
+  if (!wm || !gate_name || !down_name || !up_name) return finish(fail("[mlp_forward_q] null weight map or name"));
+  auto scales_of = [&](const char *name) -> qmm_array {
+    std::string n(name);
+    if (!ends_with(n, ".weight")) return qmm_array{nullptr};
+    return qmm_weights_get(m, (n.substr(0, n.size() - 7) + ".scales").c_str());
+  };
+  qmm_array wg = qmm_weights_get(m, gate_name), wu = qmm_weights_get(m, up_name);
+  if (!wg.ctx || !wu.ctx) return QMM_WE_MISSING_WEIGHT;
+  qmm_array sg = scales_of(gate_name), su = scales_of(up_name);
+  qmm_array h{nullptr};
+  int rc;
+  if (wm->quant.mode != QMM_QUANT_NONE && sg.ctx && su.ctx) {
+    const char *mode = wm->quant.mode == QMM_QUANT_MXFP8 ? "mxfp8" : "nvfp4";
+    rc = qmm_mlp_gate_up_silu(&h, x, wg, sg, wu, su, qmm_optional_int{(int)wm->quant.group_size, true},
+                              qmm_optional_int{(int)wm->quant.bits, true}, mode, s);
+  } else {
+    qmm_array g{nullptr}, u{nullptr};
+    rc = qmm_named_linear_q(&g, m, x, gate_name, s);
+    if (!rc) rc = qmm_named_linear_q(&u, m, x, up_name, s);
+    if (!rc) rc = qmm_silu_mul(&h, g, u, s);
+    if (g.ctx) qmm_array_free(g);
+    if (u.ctx) qmm_array_free(u);
+  }
+  if (!rc) rc = qmm_named_linear_q(res, m, h, down_name, s);
+  if (h.ctx) qmm_array_free(h);
+  return rc;
+}
+
 }  // extern "C"

@@ -121,6 +121,11 @@ _SIGS = {
     "qmm_weights_quant": (qmm_quant_spec, [qmm_weight_map]),
     "qmm_named_linear_q": (c_int, [POINTER(qmm_array), qmm_weight_map, qmm_array, c_char_p, qmm_stream]),
     "qmm_linear": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_stream]),
+    "qmm_silu_mul": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_stream]),
+    "qmm_mlp_gate_up_silu": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_array, qmm_array, qmm_array,
+                                     qmm_optional_int, qmm_optional_int, c_char_p, qmm_stream]),
+    "qmm_mlp_forward_q": (c_int, [POINTER(qmm_array), qmm_weight_map, qmm_array, c_char_p, c_char_p, c_char_p,
+                                  qmm_stream]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
@@ -302,6 +307,24 @@ def linear(x: Array, w: Array, *, out: Array | None = None, stream: Stream | Non
     return res
 
 
+def silu_mul(g: Array, u: Array, *, out: Array | None = None, stream: Stream | None = None) -> Array:
+    """silu(g) * u with the reference's per-op roundings (src/model.zig:405-415, :451-456)."""
+    res = out if out is not None else Array()
+    s = _stream(stream)
+    check(lib.qmm_silu_mul(byref(res.h), g.h, u.h, s.h), "silu_mul")
+    return res
+
+
+def mlp_gate_up_silu(x: Array, w_gate: Array, s_gate: Array, w_up: Array, s_up: Array, mode: str, *,
+                     group_size=None, bits=None, out: Array | None = None, stream: Stream | None = None) -> Array:
+    """silu(x @ deq(Wg).T) * (x @ deq(Wu).T) (src/model.zig:905-913), fused for decode shapes."""
+    res = out if out is not None else Array()
+    s = _stream(stream)
+    check(lib.qmm_mlp_gate_up_silu(byref(res.h), x.h, w_gate.h, s_gate.h, w_up.h, s_up.h, opt_int(group_size),
+                                   opt_int(bits), mode.encode(), s.h), "mlp_gate_up_silu")
+    return res
+
+
 def infer_quant_spec_json(header: str):
     b = header.encode()
     spec = qmm_quant_spec()
@@ -356,6 +379,15 @@ class WeightMap:
         rc = lib.qmm_named_linear_q(byref(res.h), self.h, x.h, name.encode(), s.h)
         if rc:
             raise QmmError(f"named_linear_q: {WE.get(rc, rc)}: {take_error()}")
+        return res
+
+    def mlp_forward_q(self, x: Array, gate: str, down: str, up: str, stream: Stream | None = None) -> Array:
+        """mlpForwardQ (src/model.zig:905-915): down(silu(gate(x)) * up(x))."""
+        res = Array()
+        s = _stream(stream)
+        rc = lib.qmm_mlp_forward_q(byref(res.h), self.h, x.h, gate.encode(), down.encode(), up.encode(), s.h)
+        if rc:
+            raise QmmError(f"mlp_forward_q: {WE.get(rc, rc)}: {take_error()}")
         return res
 
     def __del__(self):

@@ -88,6 +88,19 @@ def f64_to_bf16_bits(v: float) -> int:
     return int(lib().oracle_f64_to_bf16(float(v)))
 
 
+def f64_to_bf16_bits_vec(v: np.ndarray) -> np.ndarray:
+    """Round float64 -> bf16 bits once, nearest-even (vectorised oracle_f64_to_bf16):
+    8 significant bits via frexp / rint (exact in float64), subnormals on the
+    2^-133 grid, overflow to inf, NaN -> 0x7FC0."""
+    v = np.asarray(v, dtype=np.float64)
+    m, e = np.frexp(v)
+    q = np.ldexp(np.rint(np.ldexp(m, 8)), e - 8)
+    q = np.where(np.abs(v) < 2.0 ** -126, np.ldexp(np.rint(np.ldexp(v, 133)), -133), q)
+    with np.errstate(over="ignore", invalid="ignore"):
+        f = q.astype(np.float32)
+    return np.where(np.isnan(v), np.uint16(0x7FC0), f32_to_bf16_bits(f))
+
+
 def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
     return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
@@ -188,3 +201,17 @@ def check_tolerance(y: np.ndarray, y_ref: np.ndarray, *, rel_fro: float = 1e-3, 
         ulp = 2.0 ** (np.floor(np.log2(scale)) - 7)
         worst = max(worst, float(np.max(np.abs(y[m] - r[m])) / ulp))
     return (fro <= rel_fro and worst <= ulps), fro, worst
+
+
+def silu_mul_bf16(g_bits: np.ndarray, u_bits: np.ndarray) -> np.ndarray:
+    """mlx-runner's MLP activation on bf16 arrays, op by op (src/model.zig:405-415
+    silu = x * sigmoid(x), :451-456 mul; used by mlpForwardQ :905-915): each op's
+    result is rounded to bf16 (nearest-even).  sigmoid is evaluated in float64.
+    Inputs and output are bf16 bit patterns (uint16)."""
+    g = bf16_bits_to_f32(g_bits).astype(np.float64)
+    u = bf16_bits_to_f32(u_bits).astype(np.float64)
+    r = lambda v: bf16_bits_to_f32(f64_to_bf16_bits_vec(v)).astype(np.float64)
+    with np.errstate(over="ignore"):
+        sg = r(1.0 / (1.0 + np.exp(-g)))
+    sl = r(g * sg)
+    return f64_to_bf16_bits_vec(sl * u)

@@ -106,3 +106,31 @@ def test_loader_missing_weight_errors(tmp_path):
         wmap.named_linear_q(x, pre + "mlp.up_proj")  # no ".weight" suffix
     with pytest.raises(Q.QmmError, match="MissingWeight"):
         wmap.named_linear_q(x, pre + "mlp.gate_proj.weight")  # absent
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+@pytest.mark.parametrize("M", [1, 20])
+def test_loader_mlp_forward_q(tmp_path, mode, M):
+    """mlpForwardQ (src/model.zig:905-915): down(silu(gate(x)) * up(x)) by names,
+    against the oracle's chain on the same checkpoint bytes."""
+    rng = np.random.default_rng(40 + M)
+    N, K = 64, 256  # gate / up [N, K], down [K, N]
+    pre = "language_model.model.layers.3.mlp."
+    q = {}
+    for name, (n, k) in (("gate_proj", (N, K)), ("up_proj", (N, K)), ("down_proj", (K, N))):
+        q[name] = O.quantize(mode, O.bf16_bits_to_f32(bf16(rng.standard_normal((n, k)) * 0.05)))
+    tensors = {}
+    for name, (wq, s) in q.items():
+        tensors[pre + name + ".weight"] = ("U32", wq)
+        tensors[pre + name + ".scales"] = ("U8", s)
+    write_safetensors(tmp_path / "model-00001-of-00001.safetensors", tensors)
+    (tmp_path / "model.safetensors.index.json").write_text(
+        json.dumps({"weight_map": {k: "model-00001-of-00001.safetensors" for k in tensors}}))
+    wmap = Q.WeightMap(str(tmp_path))
+    xb = bf16(rng.standard_normal((M, K)))
+    y = wmap.mlp_forward_q(Q.Array.from_numpy(xb, Q.BFLOAT16), pre + "gate_proj.weight", pre + "down_proj.weight",
+                           pre + "up_proj.weight").numpy()
+    h = O.silu_mul_bf16(O.qmm(mode, xb, *q["gate_proj"]), O.qmm(mode, xb, *q["up_proj"]))
+    ref = O.qmm(mode, h, *q["down_proj"])
+    ok, fro, worst = O.check_tolerance(O.bf16_bits_to_f32(y), O.bf16_bits_to_f32(ref), **TOL)
+    assert ok, (fro, worst)

@@ -159,9 +159,10 @@ def test_decode_matches_oracle(mode, M, N, K):
 @pytest.mark.parametrize("mode,N,K", [("nvfp4", 13, 17408), ("nvfp4", 37, 10752), ("nvfp4", 5, 33792),
                                       ("mxfp8", 11, 17408), ("mxfp8", 29, 5632)])
 def test_decode_long_k_matches_oracle(mode, M, N, K):
-    """Rows longer than one wave's segment (the down projection, K = 17408): K split
-    across a block's lanes; N not a multiple of the block's rows, chunk counts not a
-    multiple of the block's lanes."""
+    """Rows too long for the register-staged x (the down projection, K = 17408): x
+    staged in LDS by DMA, rows streamed per wave; N not a multiple of the grid's
+    waves, chunk counts not a multiple of the segment; K = 33792 at M >= 3 does not
+    fit LDS and takes the looping kernel."""
     rng = np.random.default_rng(M * 7 + N + K)
     wq, s = rand_w(rng, mode, N, K)
     xb = bf16(rng.standard_normal((M, K)) * 0.5)
@@ -269,4 +270,44 @@ def test_dense_linear_matches_fp32_reference(M):
     ref = f32(xb).astype(np.float64) @ f32(wb).astype(np.float64).T
     refb = np.array([[O.f64_to_bf16_bits(v) for v in r] for r in ref], np.uint16)
     ok, fro, worst = O.check_tolerance(f32(y), f32(refb), **TOL)
+    assert ok, (fro, worst)
+
+
+# ---------------------------------------------------------------- MLP activation and the fused gate/up
+def test_silu_mul_matches_oracle():
+    """src/model.zig:405-415 / :451-456 on the GPU: bf16 chain within one ulp of the
+    oracle's (sigmoid in f32 here, f64 there); f32 arrays against numpy."""
+    rng = np.random.default_rng(31)
+    g = bf16(rng.standard_normal((7, 999)) * 6)
+    u = bf16(rng.standard_normal((7, 999)))
+    h = Q.silu_mul(Q.Array.from_numpy(g, Q.BFLOAT16), Q.Array.from_numpy(u, Q.BFLOAT16)).numpy()
+    ref = O.silu_mul_bf16(g, u)
+    diff = np.abs(h.astype(np.int32) - ref.astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.995
+    gf = (rng.standard_normal(4096) * 6).astype(np.float32)
+    uf = rng.standard_normal(4096).astype(np.float32)
+    hf = Q.silu_mul(Q.Array.from_numpy(gf, Q.FLOAT32), Q.Array.from_numpy(uf, Q.FLOAT32)).numpy()
+    ref_f = (gf.astype(np.float64) / (1 + np.exp(-gf.astype(np.float64)))) * uf
+    assert np.allclose(hf, ref_f, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+@pytest.mark.parametrize("M,N,K", [(1, 200, 512), (2, 96, 5120), (3, 61, 1536), (4, 48, 5120), (20, 72, 512)])
+def test_mlp_gate_up_silu_matches_oracle(mode, M, N, K):
+    """silu(x Wg^T) * (x Wu^T) (src/model.zig:905-913): fused for M <= 4, projections
+    + activation for larger M; equal to quantized_matmul x 2 + silu_mul bit for bit,
+    and within tolerance of the oracle's chain."""
+    rng = np.random.default_rng(M * 100 + N + K)
+    wg, sg = rand_w(rng, mode, N, K)
+    wu, su = rand_w(rng, mode, N, K)
+    xb = bf16(rng.standard_normal((M, K)))
+    A = lambda a, d: Q.Array.from_numpy(a, d)
+    x = A(xb, Q.BFLOAT16)
+    h = Q.mlp_gate_up_silu(x, A(wg, Q.UINT32), A(sg, Q.UINT8), A(wu, Q.UINT32), A(su, Q.UINT8), mode).numpy()
+    g = Q.quantized_matmul(x, A(wg, Q.UINT32), A(sg, Q.UINT8), mode)
+    u = Q.quantized_matmul(x, A(wu, Q.UINT32), A(su, Q.UINT8), mode)
+    h2 = Q.silu_mul(g, u).numpy()
+    assert np.array_equal(h, h2)
+    ref = O.silu_mul_bf16(O.qmm(mode, xb, wg, sg), O.qmm(mode, xb, wu, su))
+    ok, fro, worst = O.check_tolerance(f32(h), f32(ref), **TOL)
     assert ok, (fro, worst)

@@ -285,3 +285,33 @@ def test_tolerance_rejects_planted_mistakes(oracle):
         assert not ok
     ok, fro, worst = O.check_tolerance(good, good)
     assert ok and fro == 0 and worst == 0
+
+
+# ---------------------------------------------------------------- MLP activation
+def test_f64_to_bf16_vec_matches_scalar(oracle):
+    rng = np.random.default_rng(21)
+    v = np.concatenate([rng.standard_normal(2000) * 10.0 ** rng.integers(-40, 38, 2000),
+                        [0.0, -0.0, 1e-45, -3e-39, 3.4e38, -3.39e38, 1.0 + 2 ** -9, 1.0 + 3 * 2 ** -9]])
+    got = O.f64_to_bf16_bits_vec(v)
+    ref = np.array([O.f64_to_bf16_bits(x) for x in v], np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_silu_mul_matches_torch_bf16_ops():
+    """The oracle's op-by-op bf16 chain against torch's CPU bf16 ops (sigmoid, two
+    multiplies, each rounding to bf16).  torch evaluates sigmoid in float32, the
+    oracle in float64: they may differ by one bf16 ulp where the two straddle a
+    rounding boundary."""
+    rng = np.random.default_rng(22)
+    g = O.f32_to_bf16_bits(rng.standard_normal(20000).astype(np.float32) * 4)
+    u = O.f32_to_bf16_bits(rng.standard_normal(20000).astype(np.float32))
+    got = O.silu_mul_bf16(g, u)
+    gt = torch.from_numpy(g.view(np.int16)).view(torch.bfloat16)
+    ut = torch.from_numpy(u.view(np.int16)).view(torch.bfloat16)
+    ref = ((gt * torch.sigmoid(gt)) * ut).view(torch.int16).numpy().view(np.uint16)
+    diff = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.999
+    # closed forms: silu(0) = 0, large positive g -> g * u, large negative -> 0
+    z = O.f32_to_bf16_bits(np.array([0.0, 100.0, -100.0], np.float32))
+    one = O.f32_to_bf16_bits(np.array([3.0, 2.0, 5.0], np.float32))
+    assert np.array_equal(O.bf16_bits_to_f32(O.silu_mul_bf16(z, one)), np.array([0.0, 200.0, -0.0], np.float32))
