@@ -534,7 +534,7 @@ __device__ __forceinline__ int xswz(int c) {
 
 constexpr int QLONG_WAVES = 4;
 
-template <int MODE, int M, int ISEG>
+template <int MODE, int M, int ISEG, int R>
 __global__ __launch_bounds__(64 * QLONG_WAVES) void qmv_long_kernel(const uint16_t *__restrict__ x,
                                                                     const uint8_t *__restrict__ w,
                                                                     const uint8_t *__restrict__ s,
@@ -548,27 +548,33 @@ __global__ __launch_bounds__(64 * QLONG_WAVES) void qmv_long_kernel(const uint16
   const int64_t row_bytes = (MODE == MXFP8) ? (int64_t)K : (int64_t)(K >> 1);
   const int C = (int)(row_bytes >> 4);
   const int spr = (MODE == MXFP8) ? (K >> 5) : (K >> 4);
-  // this wave's rows: gw, gw + nw, gw + 2 nw, ...; work unit u = (row u / nseg, segment u % nseg)
+  // this wave's row groups (R rows each): gw, gw + nw, ...; the rows of group k are
+  // R (gw + k nw) + [0, R); work unit u = (group u / nseg, segment u % nseg)
   const int gw = blockIdx.x * QLONG_WAVES + wave, nw = gridDim.x * QLONG_WAVES;
   const int nseg = (C + 64 * ISEG - 1) / (64 * ISEG);
-  const int nrows = gw < N ? (N - 1 - gw) / nw + 1 : 0;
+  const int ngroups = (N + R - 1) / R;
+  const int nrows = gw < ngroups ? (ngroups - 1 - gw) / nw + 1 : 0;
   const int units = nrows * nseg;
 
-  auto load_unit = [&](int u, uint4 (&q)[ISEG], uint32_t (&sc)[ISEG]) __attribute__((always_inline)) {
+  auto load_unit = [&](int u, uint4 (&q)[ISEG][R], uint32_t (&sc)[ISEG][R]) __attribute__((always_inline)) {
     const int k = u / nseg, seg = u - k * nseg;
-    const int64_t n = gw + (int64_t)k * nw;
-    const uint8_t *wr = w + n * row_bytes;
-    const uint8_t *sr = s + n * spr;
+    const int64_t n0 = (int64_t)R * (gw + (int64_t)k * nw);
 #pragma unroll
-    for (int i = 0; i < ISEG; ++i) {
-      int c = seg * 64 * ISEG + lane + 64 * i;
-      c = c < C ? c : C - 1;
-      q[i] = load_stream16(wr + ((int64_t)c << 4));
-      sc[i] = (MODE == NVFP4) ? (uint32_t) * (const uint16_t *)(sr + 2 * c) : (uint32_t)sr[c >> 1];
+    for (int r = 0; r < R; ++r) {
+      const int64_t n = n0 + r < N ? n0 + r : N - 1;  // tail rows re-read row N - 1; results dropped
+      const uint8_t *wr = w + n * row_bytes;
+      const uint8_t *sr = s + n * spr;
+#pragma unroll
+      for (int i = 0; i < ISEG; ++i) {
+        int c = seg * 64 * ISEG + lane + 64 * i;
+        c = c < C ? c : C - 1;
+        q[i][r] = load_stream16(wr + ((int64_t)c << 4));
+        sc[i][r] = (MODE == NVFP4) ? (uint32_t) * (const uint16_t *)(sr + 2 * c) : (uint32_t)sr[c >> 1];
+      }
     }
   };
-  uint4 qa[ISEG], qb[ISEG];
-  uint32_t sa[ISEG], sb[ISEG];
+  uint4 qa[ISEG][R], qb[ISEG][R];
+  uint32_t sa[ISEG][R], sb[ISEG][R];
   if (units > 0) load_unit(0, qa, sa);
   if (units > 1) load_unit(1, qb, sb);
 
@@ -586,11 +592,13 @@ __global__ __launch_bounds__(64 * QLONG_WAVES) void qmv_long_kernel(const uint16
     __syncthreads();
   }
 
-  float acc[M];
+  float acc[R][M];
 #pragma unroll
-  for (int m = 0; m < M; ++m) acc[m] = 0.f;
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
 
-  auto compute_unit = [&](int u, const uint4 (&q)[ISEG], const uint32_t (&sc)[ISEG]) __attribute__((always_inline)) {
+  auto compute_unit = [&](int u, const uint4 (&q)[ISEG][R], const uint32_t (&sc)[ISEG][R]) __attribute__((always_inline)) {
     const int k = u / nseg, seg = u - k * nseg;
 #pragma unroll
     for (int i = 0; i < ISEG; ++i) {
@@ -610,55 +618,60 @@ __global__ __launch_bounds__(64 * QLONG_WAVES) void qmv_long_kernel(const uint16
           xw[m][4 * j + 2] = v.z;
           xw[m][4 * j + 3] = v.w;
         }
-      const uint32_t d[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
-      if constexpr (MODE == NVFP4) {
-        bf16x2_t wb[16];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          wb[4 * j + 0] = fp4x2_to_bf16x2<0>(d[j]);
-          wb[4 * j + 1] = fp4x2_to_bf16x2<1>(d[j]);
-          wb[4 * j + 2] = fp4x2_to_bf16x2<2>(d[j]);
-          wb[4 * j + 3] = fp4x2_to_bf16x2<3>(d[j]);
-        }
-        const float s0 = __builtin_amdgcn_cvt_f32_fp8((int)sc[i], 0);
-        const float s1 = __builtin_amdgcn_cvt_f32_fp8((int)sc[i], 1);
+      for (int r = 0; r < R; ++r) {
+        const uint32_t d[4] = {q[i][r].x, q[i][r].y, q[i][r].z, q[i][r].w};
+        if constexpr (MODE == NVFP4) {
+          bf16x2_t wb[16];
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-          float g0 = 0.f, g1 = 0.f;
+          for (int j = 0; j < 4; ++j) {
+            wb[4 * j + 0] = fp4x2_to_bf16x2<0>(d[j]);
+            wb[4 * j + 1] = fp4x2_to_bf16x2<1>(d[j]);
+            wb[4 * j + 2] = fp4x2_to_bf16x2<2>(d[j]);
+            wb[4 * j + 3] = fp4x2_to_bf16x2<3>(d[j]);
+          }
+          const float s0 = __builtin_amdgcn_cvt_f32_fp8((int)sc[i][r], 0);
+          const float s1 = __builtin_amdgcn_cvt_f32_fp8((int)sc[i][r], 1);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) g0 = dot2_bf16(wb[j], xw[m][j], g0);
+          for (int m = 0; m < M; ++m) {
+            float g0 = 0.f, g1 = 0.f;
 #pragma unroll
-          for (int j = 8; j < 16; ++j) g1 = dot2_bf16(wb[j], xw[m][j], g1);
-          const float v = __builtin_fmaf(g1, s1, g0 * s0);
-          acc[m] += valid ? v : 0.f;
-        }
-      } else {
-        bf16x2_t wb[8];
+            for (int j = 0; j < 8; ++j) g0 = dot2_bf16(wb[j], xw[m][j], g0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          wb[2 * j + 0] = fp8x2_to_bf16x2<false>(d[j]);
-          wb[2 * j + 1] = fp8x2_to_bf16x2<true>(d[j]);
-        }
-        const float s0 = e8m0_to_f32(sc[i]);
+            for (int j = 8; j < 16; ++j) g1 = dot2_bf16(wb[j], xw[m][j], g1);
+            const float v = __builtin_fmaf(g1, s1, g0 * s0);
+            acc[r][m] += valid ? v : 0.f;
+          }
+        } else {
+          bf16x2_t wb[8];
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-          float g = 0.f;
+          for (int j = 0; j < 4; ++j) {
+            wb[2 * j + 0] = fp8x2_to_bf16x2<false>(d[j]);
+            wb[2 * j + 1] = fp8x2_to_bf16x2<true>(d[j]);
+          }
+          const float s0 = e8m0_to_f32(sc[i][r]);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) g = dot2_bf16(wb[j], xw[m][j], g);
-          acc[m] += valid ? g * s0 : 0.f;
+          for (int m = 0; m < M; ++m) {
+            float g = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) g = dot2_bf16(wb[j], xw[m][j], g);
+            acc[r][m] += valid ? g * s0 : 0.f;
+          }
         }
       }
     }
-    if (seg == nseg - 1) {  // row done: reduce, lane m writes y[m, n], restart
-      const int64_t n = gw + (int64_t)k * nw;
+    if (seg == nseg - 1) {  // rows done: reduce, lane r * M + m writes y[m, n0 + r], restart
+      const int64_t n0 = (int64_t)R * (gw + (int64_t)k * nw);
       float out = 0.f;
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const float v = wave_sum(acc[m]);
-        out = lane == m ? v : out;
-        acc[m] = 0.f;
-      }
-      if (lane < M) y[(int64_t)lane * N + n] = f32_to_bf16_rne(out);
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const float v = wave_sum(acc[r][m]);
+          out = lane == r * M + m ? v : out;
+          acc[r][m] = 0.f;
+        }
+      if (lane < R * M && n0 + lane / M < N) y[(int64_t)(lane % M) * N + n0 + lane / M] = f32_to_bf16_rne(out);
     }
   };
   // two units in flight: compute one while the next one's loads land
@@ -677,13 +690,13 @@ inline size_t qmv_long_lds(int mode, int M, int K) { return (size_t)M * K * 2; }
 constexpr size_t QMV_LONG_LDS_MAX = 156 * 1024;
 
 // Blocks per CU: as many as the CU's LDS holds copies of x (1 from M * K * 2 > 78 KiB).
-template <int MODE, int M, int ISEG, int PER_CU>
+template <int MODE, int M, int ISEG, int R, int PER_CU>
 static hipError_t launch_qmv_long_t(const QmmArgs &a, hipStream_t st) {
   const size_t lds = qmv_long_lds(MODE, M, a.K);
   static bool attr_set = false;
   static int cus = 0;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)qmv_long_kernel<MODE, M, ISEG>,
+    hipError_t e = hipFuncSetAttribute((const void *)qmv_long_kernel<MODE, M, ISEG, R>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)QMV_LONG_LDS_MAX);
     if (e != hipSuccess) return e;
     int dev = 0;
@@ -693,9 +706,9 @@ static hipError_t launch_qmv_long_t(const QmmArgs &a, hipStream_t st) {
     attr_set = true;
   }
   const int per_cu = (int)(QMV_LONG_LDS_MAX / lds) < PER_CU ? (int)(QMV_LONG_LDS_MAX / lds) : PER_CU;
-  const int want = (a.N + QLONG_WAVES - 1) / QLONG_WAVES, have = cus * (per_cu > 0 ? per_cu : 1);
+  const int want = ((a.N + R - 1) / R + QLONG_WAVES - 1) / QLONG_WAVES, have = cus * (per_cu > 0 ? per_cu : 1);
   dim3 grid(want < have ? want : have);
-  hipLaunchKernelGGL((qmv_long_kernel<MODE, M, ISEG>), grid, dim3(64 * QLONG_WAVES), lds, st, (const uint16_t *)a.x,
+  hipLaunchKernelGGL((qmv_long_kernel<MODE, M, ISEG, R>), grid, dim3(64 * QLONG_WAVES), lds, st, (const uint16_t *)a.x,
                      a.w, a.s, (uint16_t *)a.y, a.N, a.K);
   return hipGetLastError();
 }
@@ -705,10 +718,10 @@ static hipError_t launch_qmv_long_t(const QmmArgs &a, hipStream_t st) {
 template <int MODE>
 static hipError_t launch_qmv_long(const QmmArgs &a, hipStream_t st) {
   switch (a.M) {
-    case 1: return launch_qmv_long_t<MODE, 1, 3, 4>(a, st);
-    case 2: return launch_qmv_long_t<MODE, 2, 5, 2>(a, st);
-    case 3: return launch_qmv_long_t<MODE, 3, 9, 1>(a, st);
-    case 4: return launch_qmv_long_t<MODE, 4, 9, 1>(a, st);
+    case 1: return launch_qmv_long_t<MODE, 1, 3, 1, 4>(a, st);
+    case 2: return launch_qmv_long_t<MODE, 2, 5, 1, 2>(a, st);
+    case 3: return launch_qmv_long_t<MODE, 3, 9, 1, 1>(a, st);
+    case 4: return launch_qmv_long_t<MODE, 4, 9, 1, 1>(a, st);
     default: return hipErrorInvalidValue;
   }
 }
