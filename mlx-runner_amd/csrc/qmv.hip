@@ -454,15 +454,20 @@ static hipError_t launch_qmv_bf16_t(const QmmArgs &a, hipStream_t st) {
   return hipGetLastError();
 }
 
-// two rows per wave (measured on the gate+up shape: 18.3 us against 19.6 us at one row)
+// Rows per wave: two where the grid stays large (the gate+up shape, N = 34816:
+// 18.3 us against 19.6 us at one row; the lm_head), one for short N, where two
+// rows leave too few blocks (N = 5120 at M = 1: 8.4 us against 6.8 us).
 // Single-segment shapes only (C <= 320 chunks: nvfp4 K <= 10240, mxfp8 K <= 5120);
-// longer rows use the looping kernel above (measured faster there).
+// longer rows use the long-row kernel.
 template <int MODE, int M>
 static hipError_t launch_qmv_bf16_m(const QmmArgs &a, hipStream_t st) {
-  constexpr int R = 2;
   const int C = MODE == MXFP8 ? a.K / 16 : a.K / 32;
-  if (C <= 3 * 64) return launch_qmv_bf16_t<MODE, M, R, 3, false>(a, st);
-  return launch_qmv_bf16_t<MODE, M, R, 5, false>(a, st);
+  if (M == 1 && a.N < 16384) {
+    if (C <= 3 * 64) return launch_qmv_bf16_t<MODE, M, 1, 3, false>(a, st);
+    return launch_qmv_bf16_t<MODE, M, 1, 5, false>(a, st);
+  }
+  if (C <= 3 * 64) return launch_qmv_bf16_t<MODE, M, 2, 3, false>(a, st);
+  return launch_qmv_bf16_t<MODE, M, 2, 5, false>(a, st);
 }
 
 template <int MODE>
