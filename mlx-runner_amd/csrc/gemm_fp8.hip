@@ -27,23 +27,6 @@ namespace qmm {
 
 // ---------------------------------------------------------------- x split pre-pass
 
-// Smallest t with 448 * 2^t >= amax (amax > 0, finite), clamped to the E8M0 range.
-__device__ __forceinline__ int ceil_scale_exp(float amax) {
-  uint32_t u = __float_as_uint(amax);
-  int e = (int)((u >> 23) & 0xFF);
-  int fl = e - 127;
-  uint32_t mant = u & 0x7FFFFFu;
-  if (e == 0) {  // f32 subnormal
-    fl = 31 - __builtin_clz(mant) - 149;
-    mant = (mant << (__builtin_clz(mant) - 8)) & 0x7FFFFFu;
-  }
-  int t = fl - 8;
-  if (mant > 0x600000u) t += 1;  // significand > 1.75: 448 * 2^(fl-8) < amax
-  if (t < -127) t = -127;
-  if (t > 127) t = 127;
-  return t;
-}
-
 // LDS / pre-tiled operand swizzle of the pipelined GEMM: 16-byte slot p of row r
 // (64 bytes of one K step) is stored at slot p ^ p_swz(r) of the row.
 __host__ __device__ __forceinline__ int p_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }

@@ -444,7 +444,10 @@ static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op) {
   if (K == 0) {
     e = launch_fill_zero(a.y, ybytes, st);
   } else if (a.M <= QMV_MAX_M) {
-    e = (aligned && qmv_fast_ok(a)) ? launch_qmv(a, st) : launch_qmv_generic(a, st);
+    if (qmv_mfma_ok(a))
+      e = launch_qmv_mfma(a, st);
+    else
+      e = (aligned && qmv_fast_ok(a)) ? launch_qmv(a, st) : launch_qmv_generic(a, st);
   } else if (aligned && gemm_mxfp8_ok(a)) {
     void *ws = nullptr;
     if (alloc_device(&ws, gemm_mxfp8_workspace(a), st)) return 1;
@@ -573,7 +576,16 @@ int qmm_mlp_gate_up_silu(qmm_array *res, qmm_array x, qmm_array w_gate, qmm_arra
   a.s = (const uint8_t *)((Arr *)s_gate.ctx)->data;
   a.y = ha->data;
   const uint8_t *wu = (const uint8_t *)((Arr *)w_up.ctx)->data, *su = (const uint8_t *)((Arr *)s_up.ctx)->data;
-  if (K > 0 && qmv_mlp_ok(a) && ((uintptr_t)wu & 15) == 0) {
+  // decode shapes: one kernel for both projections and the activation.  Each
+  // fused kernel computes the same per-row sums as the kernel run_qmm picks
+  // for the shape, so the fused result equals the unfused one.
+  if (K > 0 && qmv_mfma_ok(a)) {
+    if (qmv_mfma_mlp_ok(a, wu, su)) {
+      hipError_t e = launch_qmv_mfma_mlp(a, wu, su, st);
+      if (e != hipSuccess) return finish(fail_hip(e, op));
+      return finish(0);
+    }
+  } else if (K > 0 && qmv_mlp_ok(a) && ((uintptr_t)wu & 15) == 0) {
     hipError_t e = launch_qmv_mlp(a, wu, su, st);
     if (e != hipSuccess) return finish(fail_hip(e, op));
     return finish(0);

@@ -112,6 +112,23 @@ __device__ __forceinline__ float silu_mul_bf16(float g, float u) {
   return bf16_round(sl * ub);
 }
 
+// Smallest t with 448 * 2^t >= amax (amax > 0, finite), clamped to the E8M0 range.
+__device__ __forceinline__ int ceil_scale_exp(float amax) {
+  uint32_t u = __float_as_uint(amax);
+  int e = (int)((u >> 23) & 0xFF);
+  int fl = e - 127;
+  uint32_t mant = u & 0x7FFFFFu;
+  if (e == 0) {  // f32 subnormal
+    fl = 31 - __builtin_clz(mant) - 149;
+    mant = (mant << (__builtin_clz(mant) - 8)) & 0x7FFFFFu;
+  }
+  int t = fl - 8;
+  if (mant > 0x600000u) t += 1;  // significand > 1.75: 448 * 2^(fl-8) < amax
+  if (t < -127) t = -127;
+  if (t > 127) t = 127;
+  return t;
+}
+
 // Sum over the 64 lanes of a wave; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

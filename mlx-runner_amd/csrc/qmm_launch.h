@@ -22,6 +22,11 @@ struct QmmArgs {
 bool qmv_fast_ok(const QmmArgs &a);
 hipError_t launch_qmv(const QmmArgs &a, hipStream_t st);
 hipError_t launch_qmv_generic(const QmmArgs &a, hipStream_t st);
+// Decode GEMV on the scaled MFMA (K = 5120; nvfp4 M <= 2, mxfp8 M <= 4, bf16 x).
+bool qmv_mfma_ok(const QmmArgs &a);
+hipError_t launch_qmv_mfma(const QmmArgs &a, hipStream_t st);
+bool qmv_mfma_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up);
+hipError_t launch_qmv_mfma_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st);
 bool qmv_mlp_ok(const QmmArgs &a);
 hipError_t launch_qmv_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st);
 hipError_t launch_silu_mul(const void *g, const void *u, void *h, int64_t n, bool f32, hipStream_t st);

@@ -1,0 +1,435 @@
+// Decode GEMV on the gfx950 scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4):
+// y[m, n] = sum_k x[m, k] * deq(W)[n, k] for M = 1..4, bf16 x, K = 512 * Q.
+//
+// The shapes are mlx-runner's per-token qmm calls with K = 5120
+// (src/model.zig:906-908 gate/up, :929-944 q/k/v, :1066-1074, :1309 lm_head;
+// M = 1 decode, 2-3 MTP verify).  They are HBM-bound.  This path moves the
+// per-element decode work off the VALU so that it no longer competes with the
+// weight stream:
+//
+//   * W is the MFMA's B operand in its stored form: E2M1 nibbles (nvfp4) or
+//     E4M3 bytes (mxfp8), never unpacked.  Lane (n, h) of the 16x16x128 MFMA
+//     holds row n; the E2M1 operand of lane group h is logical K [32h, 32h+32),
+//     the E4M3 operand bytes 0-15 / 16-31 are K 16h + [0,16) / 64 + 16h + [0,16)
+//     (both measured on gfx950), so the B operands are plain byte ranges of a row.
+//   * x is split into E4M3 hi + lo with a shared exponent per scale group:
+//     hi = x with its mantissa cut to 3 bits, lo = x - hi.  Both are exact E4M3
+//     values (4 significant bits) for every element within 2^13 of the group
+//     maximum, so hi + lo = x exactly there; smaller elements round at 2^-21 of
+//     the group maximum.
+//   * mxfp8: W's E8M0 group scale and x's hi/lo exponents are the MFMA's own
+//     block scales; columns (m, hi|lo) of x accumulate over K in the MFMA and
+//     y = column hi + column lo.
+//   * nvfp4: the E4M3 group scales (one per 16 elements) are not block scales
+//     of the MFMA, so x is laid out block-diagonally: column (g, hi|lo) of the A
+//     operand holds x only on group g of the 128-element chunk, output column
+//     (g, .) is the group's partial dot product, and W's E4M3 byte scales it in
+//     fp32: 5 VALU ops per 16 rows x 128 K (the unpacking GEMV needs ~36 per
+//     2048 elements).
+//
+// Work split: one workgroup per CU owns a contiguous range of rows (N spread
+// evenly, so every CU reads the same number of HBM bytes).  Wave q owns the K
+// slice [512q, 512q + 512) and keeps the A operands of its 4 chunks in
+// registers for the whole kernel; the waves walk the range's 16-row blocks in
+// step.  Per row block a wave loads its slice with contiguous 1 KiB loads,
+// passes it through a private LDS tile into the MFMA layout, and writes 16
+// partial sums to LDS; the partials are summed over the waves in a fixed
+// order, so the result is deterministic.
+#include "qmm_device.h"
+#include "qmm_launch.h"
+
+namespace qmm {
+
+namespace {
+
+constexpr int QF_REC = 272;  // x record of one (x row, 128-K chunk): 256 data bytes, then 16 zero bytes
+constexpr int QF_FLUSH_MAX = 16;
+
+// Keeps a value in its own register until this point.  The scale operands of
+// v_mfma_scale_* are read after the instruction issues; the compiler does not
+// treat them as in use by the MFMA and may rewrite the register right after
+// it (measured: a later chunk's scale then applied to an earlier chunk).  Each
+// MFMA's scale therefore stays live until the row block's results are read.
+__device__ __forceinline__ void keep_live(int v) { asm volatile("" ::"v"(v)); }
+
+// Workgroup barrier for LDS data only.  __syncthreads() also orders global memory,
+// which on gfx950 means waiting for every load in flight (vmcnt(0)): the weight
+// stream would drain at each barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// E4M3 hi/lo of 8 consecutive bf16 (one 16-byte piece).  GT lanes share a scale
+// group (2: 16 elements, 4: 32 elements) and must be adjacent and all active.
+template <int GT>
+__device__ __forceinline__ void split8(const uint4 q, uint2 &hi, uint2 &lo, int &th, int &tl) {
+  const uint32_t wv[4] = {q.x, q.y, q.z, q.w};
+  float xf[8], hf[8];
+  float amax = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    xf[2 * t] = __uint_as_float(wv[t] << 16);
+    xf[2 * t + 1] = __uint_as_float(wv[t] & 0xFFFF0000u);
+    const uint32_t hb = wv[t] & 0xFFF0FFF0u;  // sign, exponent, top 3 mantissa bits
+    hf[2 * t] = __uint_as_float(hb << 16);
+    hf[2 * t + 1] = __uint_as_float(hb & 0xFFFF0000u);
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) amax = fmaxf(amax, fabsf(xf[t]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  if (GT == 4) amax = fmaxf(amax, __shfl_xor(amax, 2));
+  th = amax > 0.f ? ceil_scale_exp(amax) : -127;  // amax * 2^-th <= 448
+  // |lo| < 2^(e-3) for an element of exponent e <= e(amax), so lo * 2^-(th-3) < 256
+  tl = th - 3 < -127 ? -127 : th - 3;
+  uint32_t hw[2], lw[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    int c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(hf[4 * t], -th), __builtin_ldexpf(hf[4 * t + 1], -th), 0,
+                                            false);
+    c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(hf[4 * t + 2], -th), __builtin_ldexpf(hf[4 * t + 3], -th), c,
+                                        true);
+    hw[t] = (uint32_t)c;
+    int d = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(xf[4 * t] - hf[4 * t], -tl),
+                                            __builtin_ldexpf(xf[4 * t + 1] - hf[4 * t + 1], -tl), 0, false);
+    d = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(xf[4 * t + 2] - hf[4 * t + 2], -tl),
+                                        __builtin_ldexpf(xf[4 * t + 3] - hf[4 * t + 3], -tl), d, true);
+    lw[t] = (uint32_t)d;
+  }
+  hi = make_uint2(hw[0], hw[1]);
+  lo = make_uint2(lw[0], lw[1]);
+}
+
+// A unit is one wave's K slice (512 elements = 4 chunks of 128) of one 16-row block:
+//   nvfp4: 16 rows x 256 bytes = 4 loads of 1 KiB (4 rows x 256 contiguous bytes each)
+//   mxfp8: 16 rows x 512 bytes = 8 loads of 1 KiB (2 rows x 512 contiguous bytes each)
+// plus its scale bytes (nvfp4 16 x 32, mxfp8 16 x 16).  Contiguous 1 KiB loads
+// stream HBM well; the MFMA operand layout (16 rows x 64 bytes per instruction)
+// read straight from HBM does not (measured 6.1-7.0 against 4.8-5.2 TB/s), so
+// each unit passes through the wave's LDS tile to change layout.
+template <int MODE>
+struct QfGeom {
+  static constexpr int UB = MODE == NVFP4 ? 256 : 512;  // W bytes per row per unit
+  static constexpr int PITCH = UB + 16;                 // tile row pitch: rows land on distinct banks
+  static constexpr int LOADS = 16 * UB / 1024;          // 1 KiB loads per unit
+  static constexpr int SB = MODE == NVFP4 ? 32 : 16;    // scale bytes per row per unit
+  static constexpr int TILE = 16 * PITCH + 16 * SB;
+  static constexpr int PREP = 4 * 4 * QF_REC + 4 * 64;  // x records (M <= 4 rows x 4 chunks) + exponents
+  static constexpr int WAVE_LDS = TILE > PREP ? TILE : PREP;
+};
+
+template <int MODE>
+constexpr size_t qf_lds_bytes(int M, int Q, int F, int nmat) {
+  return (size_t)Q * QfGeom<MODE>::WAVE_LDS + (size_t)F * nmat * M * Q * 16 * 4;
+}
+
+// NMAT = 2 is the MLP form (src/model.zig:905-915): W (gate) and W2 (up) are
+// walked row block by row block, unit (rb, 0) then (rb, 1), and the flush
+// writes silu(gate) * up with the reference's bf16 roundings.  The per-row sums
+// are the same as those of two separate NMAT = 1 launches, so fused and
+// unfused results are identical.  D: units whose weights are in flight.
+template <int MODE, int M, int Q, int NMAT, int D>
+__global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__restrict__ x,
+                                                          const uint8_t *__restrict__ w,
+                                                          const uint8_t *__restrict__ s, const uint8_t *__restrict__ w2,
+                                                          const uint8_t *__restrict__ s2, uint16_t *__restrict__ y,
+                                                          int N, int K, int F) {
+  using G = QfGeom<MODE>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
+  uint8_t *tile = lds + q * G::WAVE_LDS;
+  float *part = (float *)(lds + Q * G::WAVE_LDS);  // [F][NMAT][M][Q][16] partial sums
+  const int r_begin = (int)((int64_t)N * blockIdx.x / gridDim.x);
+  const int r_end = (int)((int64_t)N * (blockIdx.x + 1) / gridDim.x);
+  const int nrb = (r_end - r_begin + 15) >> 4;
+  const int k0 = 512 * q;  // this wave's K slice
+
+  // 1) x of the slice: lane l holds elements [8l, 8l+8) of each row m
+  uint4 xr[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) xr[m] = *(const uint4 *)(x + (int64_t)m * K + k0 + 8 * lane);
+
+  // 2) the first unit's weights.  Load i, lane l: nvfp4 row 4i + l/16, bytes 16 (l%16);
+  //    mxfp8 row 2i + l/32, bytes 16 (l%32).  Scales: lane l, row l/4, bytes (l%4) SB/4.
+  constexpr int RPL = MODE == NVFP4 ? 4 : 2;  // rows per load
+  constexpr int LPR = 64 / RPL;               // lanes per row
+  const int64_t wrow = MODE == NVFP4 ? (K >> 1) : K, srow = MODE == NVFP4 ? (K >> 4) : (K >> 5);
+  const int wcol = q * G::UB + 16 * (lane % LPR);
+  const int scol = q * G::SB + (lane & 3) * (G::SB / 4);
+  auto row_of = [&](int rb, int rr) __attribute__((always_inline)) {
+    const int row = r_begin + 16 * rb + rr;
+    return row < r_end ? row : r_end - 1;  // rows past the range re-read its last row (results dropped)
+  };
+  // unit u = (row block u / NMAT, matrix u % NMAT) lives in buffer u % D
+  uint4 wv[D][G::LOADS];
+  uint32_t sv0[D], sv1[D];
+  auto load_unit = [&](int u, int buf) __attribute__((always_inline)) {
+    const int rb = u / NMAT, mat = u % NMAT;
+    const uint8_t *wm = mat ? w2 : w, *sm = mat ? s2 : s;
+#pragma unroll
+    for (int i = 0; i < G::LOADS; ++i)
+      wv[buf][i] = load_stream16(wm + row_of(rb, RPL * i + lane / LPR) * wrow + wcol);
+    const uint8_t *sp = sm + row_of(rb, lane >> 2) * srow + scol;
+    if constexpr (MODE == NVFP4) {
+      const uint2 t2 = *(const uint2 *)sp;
+      sv0[buf] = t2.x;
+      sv1[buf] = t2.y;
+    } else {
+      sv0[buf] = *(const uint32_t *)sp;
+      sv1[buf] = 0;
+    }
+  };
+  load_unit(0, 0);
+
+  // 3) x split into records in this wave's tile (before it holds weights), then the
+  //    A operands of the slice's 4 chunks into registers, kept for the whole kernel.
+  uint8_t *ex = tile + 4 * 4 * QF_REC;  // exponent bytes, 64 per x row
+  {
+    const int c = lane >> 4, kc = (lane & 15) * 8;  // chunk of the slice, offset in the chunk
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      uint2 hi, lo;
+      int th, tl;
+      split8<MODE == NVFP4 ? 2 : 4>(xr[m], hi, lo, th, tl);
+      uint8_t *rec = tile + (m * 4 + c) * QF_REC;
+      if constexpr (MODE == NVFP4) {
+        // group g of the chunk: hi at 32 g, lo at 32 g + 16; exponents [m][g][hl][c]
+        const int g = kc >> 4, half = (kc >> 3) & 1;
+        *(uint2 *)(rec + 32 * g + 8 * half) = hi;
+        *(uint2 *)(rec + 32 * g + 16 + 8 * half) = lo;
+        if (half == 0) {
+          ex[m * 64 + (g * 2 + 0) * 4 + c] = (uint8_t)(th + 127);
+          ex[m * 64 + (g * 2 + 1) * 4 + c] = (uint8_t)(tl + 127);
+        }
+      } else {
+        // hi at [0, 128), lo at [128, 256) in K order; exponents [m][hl][c][block]
+        *(uint2 *)(rec + kc) = hi;
+        *(uint2 *)(rec + 128 + kc) = lo;
+        if ((kc & 31) == 0) {
+          ex[m * 64 + (0 * 4 + c) * 4 + (kc >> 5)] = (uint8_t)(th + 127);
+          ex[m * 64 + (1 * 4 + c) * 4 + (kc >> 5)] = (uint8_t)(tl + 127);
+        }
+      }
+    }
+    if (lane < 4 * M) *(uint4 *)(tile + lane * QF_REC + 256) = make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int d = 1; d < D; ++d) load_unit(d, d);
+  // A-operand addressing of this lane (row n = lane % 16 of the A operand).
+  //   E4M3 A layout: lane group h, byte t holds logical K 64 (t/16) + 16 h + t%16.
+  const int h = lane >> 4, n = lane & 15;
+  constexpr int MA = MODE == NVFP4 ? M : 1;  // A operands per chunk
+  i32x8_t areg[4][MA];
+  int asreg[4][MA];
+  {
+    int aoff0, aoff1, am, ebase;
+    if constexpr (MODE == NVFP4) {
+      // column n = 4p + v: group g = 2p + v/2 of the chunk, hi (v even) or lo; nonzero only
+      // where logical K is in group g, i.e. lane group g%4, byte half g/4
+      const int p = n >> 2, v = n & 3, g = 2 * p + (v >> 1), hl = v & 1;
+      const bool own = h == (g & 3);
+      aoff0 = own && g < 4 ? 32 * g + 16 * hl : 256;
+      aoff1 = own && g >= 4 ? 32 * g + 16 * hl : 256;
+      am = 0;
+      ebase = (g * 2 + hl) * 4;  // + m*64 + c
+    } else {
+      // column n = 2m + hl for m < M; the other columns are zero
+      const int m = n >> 1, hl = n & 1;
+      const bool live = m < M;
+      aoff0 = live ? 128 * hl + 16 * h : 256;
+      aoff1 = live ? 128 * hl + 64 + 16 * h : 256;
+      am = live ? m : 0;
+      ebase = am * 64 + hl * 16 + h;  // + 4c: block h of chunk c
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int m = 0; m < MA; ++m) {
+        const uint8_t *rec = tile + ((MODE == NVFP4 ? m : am) * 4 + c) * QF_REC;
+        const uint4 u0 = *(const uint4 *)(rec + aoff0), u1 = *(const uint4 *)(rec + aoff1);
+        areg[c][m] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+        asreg[c][m] = MODE == NVFP4 ? ex[m * 64 + ebase + c] : ex[ebase + 4 * c];
+      }
+  }
+
+  // sum the waves' partials of row blocks [rb_first, rb_last] in wave order
+  auto flush = [&](int rb_first, int rb_last) __attribute__((always_inline)) {
+    lds_barrier();
+    const int items = (rb_last - rb_first + 1) * M * 16;
+    for (int t = tid; t < items; t += 64 * Q) {
+      const int nn = t & 15, m = (t >> 4) % M, rbi = (t >> 4) / M;
+      const int rb = rb_first + rbi, row = r_begin + 16 * rb + nn;
+      float sum[NMAT];
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat) {
+        const float *pp = part + ((((rb % F) * NMAT + mat) * M + m) * Q) * 16 + nn;
+        sum[mat] = 0.f;
+#pragma unroll
+        for (int qq = 0; qq < Q; ++qq) sum[mat] += pp[16 * qq];
+      }
+      const float out = NMAT == 2 ? silu_mul_bf16(sum[0], sum[NMAT - 1]) : sum[0];
+      if (row < r_end) y[(int64_t)m * N + row] = f32_to_bf16_rne(out);
+    }
+    lds_barrier();
+  };
+
+  uint8_t *wt = tile, *st = tile + 16 * G::PITCH;
+  const int units = nrb * NMAT;
+  // units go in groups of D so that buffer indices are static; the units past
+  // the last one are computed too (clamped rows): loads and MFMAs under a branch
+  // make the compiler's wait counting conservative.
+  for (int u0 = 0; u0 < units; u0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int u = u0 + d, rb = u / NMAT, mat = u % NMAT;
+      // unit u: registers -> tile (the x records are no longer needed there), then refill
+      // the buffer with unit u + D (past the last unit: clamped rows, unused)
+#pragma unroll
+      for (int i = 0; i < G::LOADS; ++i)
+        *(uint4 *)(wt + (RPL * i + lane / LPR) * G::PITCH + 16 * (lane % LPR)) = wv[d][i];
+      if constexpr (MODE == NVFP4)
+        *(uint2 *)(st + 8 * lane) = make_uint2(sv0[d], sv1[d]);
+      else
+        *(uint32_t *)(st + 4 * lane) = sv0[d];
+      load_unit(u + D, d);
+      const bool live = u < units;
+      const int rbf = rb % F;
+      float *pslot = part + ((rbf * NMAT + mat) * M) * Q * 16;
+      if constexpr (MODE == NVFP4) {
+        float acc[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          // B operand: row n, bytes [64c + 16h, +16) of the unit; scales of groups 2h, 2h+1
+          const uint4 b = *(const uint4 *)(wt + n * G::PITCH + 64 * c + 16 * h);
+          const i32x8_t bw = {(int)b.x, (int)b.y, (int)b.z, (int)b.w, 0, 0, 0, 0};
+          const f32x2_t sc =
+              __builtin_amdgcn_cvt_pk_f32_fp8((int)*(const uint16_t *)(st + n * G::SB + 8 * c + 2 * h), false);
+          f32x4_t dd[M];
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+            dd[m] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(areg[c][m], bw, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0,
+                                                                     4, 0, asreg[c][m], 0, 127);
+          // lane (n, h) holds columns 4h..4h+3: groups 2h (hi, lo) and 2h+1 (hi, lo)
+#pragma unroll
+          for (int m = 0; m < M; ++m) acc[m] += sc.x * (dd[m][0] + dd[m][1]) + sc.y * (dd[m][2] + dd[m][3]);
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          float a = acc[m];
+          a += __shfl_xor(a, 16);
+          a += __shfl_xor(a, 32);
+          if (live && h == 0) pslot[(m * Q + q) * 16 + n] = a;
+        }
+      } else {
+        f32x4_t dd = {0.f, 0.f, 0.f, 0.f};
+        int bsc[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          // E4M3 B operand: bytes 0-15 are K offsets 16h + [0,16) of the chunk, bytes 16-31
+          // are 64 + 16h + [0,16); block h's scale is byte 4c + h of row n's scales
+          const uint8_t *bp = wt + n * G::PITCH + 128 * c + 16 * h;
+          const uint4 b0 = *(const uint4 *)bp, b1 = *(const uint4 *)(bp + 64);
+          const i32x8_t bw = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+          bsc[c] = st[n * G::SB + 4 * c + h];
+          dd = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(areg[c][0], bw, dd, 0, 0, 0, asreg[c][0], 0, bsc[c]);
+        }
+        // lane (n, h) holds columns 4h + v = (m = 2h + v/2, hi | lo)
+#pragma unroll
+        for (int v2 = 0; v2 < 2; ++v2) {
+          const int m = 2 * h + v2;
+          if (live && m < M) pslot[(m * Q + q) * 16 + n] = dd[2 * v2] + dd[2 * v2 + 1];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) keep_live(bsc[c]);
+      }
+      if (live && mat == NMAT - 1 && ((rb + 1) % F == 0 || rb + 1 == nrb)) flush(rb - rbf, rb);
+    }
+  }
+}
+
+}  // namespace
+
+// Waves per workgroup for K: one per 512-element slice.
+static int qf_waves(int K) { return (K > 0 && K % 512 == 0 && K / 512 <= 16) ? K / 512 : 0; }
+
+bool qmv_mfma_ok(const QmmArgs &a) {
+  if (a.x_f32 || a.M < 1 || a.N < 16) return false;
+  if (a.M > (a.mode == NVFP4 ? 2 : 4)) return false;  // nvfp4 M = 3, 4 would not fit the A operands in registers
+  if (qf_waves(a.K) != 10) return false;              // instantiated for K = 5120
+  // Where this path is faster than the unpacking GEMV (measured on the 256-CU
+  // MI355X, K = 5120): at M = 1 only for nvfp4 with many rows per CU (it pays a
+  // per-workgroup x split and pipeline fill; mxfp8 decodes at 1 VALU op per
+  // weight byte and streams at HBM speed either way), at M >= 2 from N = 4096.
+  if (a.M == 1 && (a.mode != NVFP4 || a.N < 16384)) return false;
+  if (a.N < 4096) return false;
+  if ((((uintptr_t)a.x) | ((uintptr_t)a.w)) & 15) return false;
+  if (((uintptr_t)a.s) & 7) return false;  // scale slices are read as 8 (nvfp4) / 4 (mxfp8) bytes
+  return true;
+}
+
+bool qmv_mfma_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up) {
+  return qmv_mfma_ok(a) && (((uintptr_t)w_up) & 15) == 0 && (((uintptr_t)s_up) & 7) == 0;
+}
+
+template <int MODE, int M, int NMAT, int D>
+static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
+                            hipStream_t st) {
+  constexpr int Q = 10;
+  auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D>;
+  const size_t lds = qf_lds_bytes<MODE>(M, Q, F, NMAT);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), lds, st, (const uint16_t *)a.x, a.w, a.s, w2, s2,
+                     (uint16_t *)a.y, a.N, a.K, F);
+  return hipGetLastError();
+}
+
+// Two units in flight per wave when each workgroup has few row blocks (the call
+// is then a few memory latencies long); one otherwise, which streams faster.
+template <int MODE, int M, int NMAT>
+static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F, int nrb,
+                              hipStream_t st) {
+  if (nrb * NMAT <= 4) return launch_qf<MODE, M, NMAT, 2>(a, w2, s2, grid, F, st);
+  return launch_qf<MODE, M, NMAT, 1>(a, w2, s2, grid, F, st);
+}
+
+template <int NMAT>
+static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, hipStream_t st) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+  }
+  const int rbs = (a.N + 15) / 16;
+  const int grid = rbs < cus ? rbs : cus;
+  const int rows_max = (a.N + grid - 1) / grid;
+  const int nrb = (rows_max + 15) / 16;
+  const int F = nrb < QF_FLUSH_MAX ? nrb : QF_FLUSH_MAX;
+  if (a.mode == NVFP4) {
+    if (a.M == 1) return launch_qf_d<NVFP4, 1, NMAT>(a, w2, s2, grid, F, nrb, st);
+    return launch_qf_d<NVFP4, 2, NMAT>(a, w2, s2, grid, F, nrb, st);
+  }
+  switch (a.M) {
+    case 1: return launch_qf_d<MXFP8, 1, NMAT>(a, w2, s2, grid, F, nrb, st);
+    case 2: return launch_qf_d<MXFP8, 2, NMAT>(a, w2, s2, grid, F, nrb, st);
+    case 3: return launch_qf_d<MXFP8, 3, NMAT>(a, w2, s2, grid, F, nrb, st);
+    default: return launch_qf_d<MXFP8, 4, NMAT>(a, w2, s2, grid, F, nrb, st);
+  }
+}
+
+hipError_t launch_qmv_mfma(const QmmArgs &a, hipStream_t st) {
+  if (!qmv_mfma_ok(a)) return hipErrorInvalidValue;
+  return launch_qf_any<1>(a, a.w, a.s, st);
+}
+
+hipError_t launch_qmv_mfma_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st) {
+  if (!qmv_mfma_mlp_ok(a, w_up, s_up)) return hipErrorInvalidValue;
+  return launch_qf_any<2>(a, w_up, s_up, st);
+}
+
+}  // namespace qmm

@@ -311,3 +311,78 @@ def test_mlp_gate_up_silu_matches_oracle(mode, M, N, K):
     ref = O.silu_mul_bf16(O.qmm(mode, xb, wg, sg), O.qmm(mode, xb, wu, su))
     ok, fro, worst = O.check_tolerance(f32(h), f32(ref), **TOL)
     assert ok, (fro, worst)
+
+
+def rand_packed(rng, mode, N, K, period=4099):
+    """Random packed weights over every code: all E2M1 nibbles (nvfp4) or every finite
+    E4M3 byte with |v| < 2 (mxfp8), with group scales in a moderate range.  Rows
+    repeat with a period of 4099 (not a multiple of the 16-row blocks) to keep
+    generation fast at large N."""
+    R = min(N, period)
+    if mode == "nvfp4":
+        wq = np.frombuffer(rng.bytes(R * K // 2), np.uint32).reshape(R, K // 8)
+        s = rng.integers(0x20, 0x48, size=(R, K // 16), dtype=np.uint8)  # E4M3 2^-4 .. 2^1
+    else:
+        b = np.frombuffer(rng.bytes(R * K), np.uint8) & 0xBF  # exponent field <= 7: no NaN code, |v| < 2
+        wq = b.view(np.uint32).reshape(R, K // 4)
+        s = rng.integers(118, 132, size=(R, K // 32), dtype=np.uint8)  # E8M0 2^-9 .. 2^4
+    if N > R:
+        wq = np.resize(wq, (N, wq.shape[1]))
+        s = np.resize(s, (N, s.shape[1]))
+    return np.ascontiguousarray(wq), np.ascontiguousarray(s)
+
+
+def make_x(rng, M, K, kind):
+    """bf16 x ~ N(0,1); "edge" plants groups that stress the E4M3 hi/lo split: zeros,
+    one value 2^23 above the rest of its group, bf16 subnormals, a wide linear ramp,
+    a group scaled by 1e-6.  Magnitudes stay O(10) so errors elsewhere stay visible."""
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if kind == "edge":
+        x[:, 0:16] = 0.0
+        x[:, 16:32] = 1e-6
+        x[:, 20] = 8.0
+        x[:, 32:48] = np.float32(2.0 ** -130)  # bf16 subnormal
+        x[:, 48:64] = np.linspace(-12.0, 12.0, 16, dtype=np.float32)
+        x[:, 96:128] *= 1e-6
+    return bf16(x)
+
+
+# Shapes above the MFMA decode path's thresholds (K = 5120: nvfp4 M = 1 from
+# N = 16384, M >= 2 from N = 4096): ragged row blocks (N % 16 != 0), and a row
+# range per workgroup long enough (N = 70001) to need several partial-sum flushes.
+@pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 1, 70001), ("nvfp4", 2, 4099),
+                                      ("nvfp4", 2, 16384), ("mxfp8", 2, 4101), ("mxfp8", 3, 8192),
+                                      ("mxfp8", 4, 4096), ("mxfp8", 4, 70001)])
+@pytest.mark.parametrize("xkind", ["normal", "edge"])
+def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
+    K = 5120
+    rng = np.random.default_rng(N * 10 + M)
+    wq, s = rand_packed(rng, mode, N, K)
+    xb = make_x(rng, M, K, xkind)
+    y = run_qmm(mode, xb, wq, s)
+    cols = np.unique(np.concatenate([np.arange(0, N, 7), np.arange(N - 40, N), np.arange(40)]))
+    ref = O.qmm(mode, xb, wq, s, cols=cols)
+    ok, fro, worst = O.check_tolerance(f32(y[:, cols]), f32(ref), **TOL)
+    assert ok, (fro, worst)
+    assert np.array_equal(run_qmm(mode, xb, wq, s), y)
+
+
+@pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 2, 4099), ("mxfp8", 3, 4101)])
+def test_mlp_gate_up_silu_mfma_shapes(mode, M, N):
+    """The fused MLP on the MFMA path: equal to two quantized_matmul + silu_mul bit for
+    bit, and within tolerance of the oracle's chain on a row sample."""
+    K = 5120
+    rng = np.random.default_rng(N + 7 * M)
+    wg, sg = rand_packed(rng, mode, N, K)
+    wu, su = rand_packed(rng, mode, N, K)
+    xb = make_x(rng, M, K, "edge")
+    A = lambda a, d: Q.Array.from_numpy(a, d)
+    x = A(xb, Q.BFLOAT16)
+    h = Q.mlp_gate_up_silu(x, A(wg, Q.UINT32), A(sg, Q.UINT8), A(wu, Q.UINT32), A(su, Q.UINT8), mode).numpy()
+    g = Q.quantized_matmul(x, A(wg, Q.UINT32), A(sg, Q.UINT8), mode)
+    u = Q.quantized_matmul(x, A(wu, Q.UINT32), A(su, Q.UINT8), mode)
+    assert np.array_equal(h, Q.silu_mul(g, u).numpy())
+    cols = np.unique(np.concatenate([np.arange(0, N, 5), np.arange(N - 20, N)]))
+    ref = O.silu_mul_bf16(O.qmm(mode, xb, wg, sg, cols=cols), O.qmm(mode, xb, wu, su, cols=cols))
+    ok, fro, worst = O.check_tolerance(f32(h[:, cols]), f32(ref), **TOL)
+    assert ok, (fro, worst)
