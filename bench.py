@@ -57,6 +57,12 @@ CONFIGS = {
     "dense_lmhead": dict(mode="bf16", M=1, N=248320, K=5120, xscale=1.0,
                          workload="dense bf16 lm_head decode GEMV (mxfp8 checkpoints), x bf16 [1,5120], "
                                   "W bf16 [248320,5120]"),
+    "gdn_decode": dict(gdn=True, B=1, T=1, Hk=16, Hv=48, Dk=128, Dv=128,
+                       workload="GDN recurrence decode step (src/gdn_packed.metal): B=1, T=1, Hk=16, Hv=48, "
+                                "Dk=Dv=128, bf16 q/k/v/beta, f32 g and state [1,48,128,128]"),
+    "gdn_prefill": dict(gdn=True, B=1, T=2048, Hk=16, Hv=48, Dk=128, Dv=128,
+                        workload="GDN recurrence over a 2048-token prefill chunk: B=1, T=2048, Hk=16, Hv=48, "
+                                 "Dk=Dv=128, bf16 q/k/v/beta, f32 g and state"),
 }
 DEFAULT = "gateup"
 BITS = {"mxfp8": 8, "nvfp4": 4, "bf16": 16}
@@ -124,6 +130,129 @@ def cpu_baseline(cfg, xb, wq, s, budget_s=12.0):
                 us_per_call=round(dt * 1e6, 1))
 
 
+def gdn_bytes(cfg):
+    """Algorithmic bytes of one GDN call: state in and out (f32), q, k, v, y (bf16), g (f32), beta (bf16)."""
+    B, T, Hk, Hv, Dk, Dv = (cfg[k] for k in ("B", "T", "Hk", "Hv", "Dk", "Dv"))
+    return 2 * 4 * B * Hv * Dv * Dk + 2 * 2 * B * T * Hk * Dk + 2 * 2 * B * T * Hv * Dv + (4 + 2) * B * T * Hv
+
+
+def gdn_flops(cfg):
+    """Per step and state row: decay (Dk mul), two dot products and the update (3 Dk FMA)."""
+    B, T, Hv, Dk, Dv = (cfg[k] for k in ("B", "T", "Hv", "Dk", "Dv"))
+    return B * T * Hv * Dv * 7 * Dk
+
+
+def replay_timed(step, steps):
+    """Capture `steps` calls in a HIP graph, settle the clocks, time one replay (ms per call)."""
+    import torch
+
+    import qmm as Q
+
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        step(0, Q.Stream.torch_current())
+        torch.cuda.current_stream().synchronize()
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(steps):
+                step(i, Q.Stream.torch_current())
+    torch.cuda.synchronize()
+    prev, t_end = None, time.perf_counter() + 0.5
+    while True:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        cur = e0.elapsed_time(e1)
+        if (prev is not None and abs(cur - prev) <= 0.03 * prev) or time.perf_counter() > t_end:
+            break
+        prev = cur
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    g.replay()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def bench_gdn(args, cfg):
+    """The GDN recurrence (qmm_gdn_recurrence): states rotate over >= 512 MiB of copies so each
+    call reads its state from HBM; each call updates its state in place."""
+    import numpy as np
+    import torch
+
+    import qmm as Q
+
+    B, T, Hk, Hv, Dk, Dv = (cfg[k] for k in ("B", "T", "Hk", "Hv", "Dk", "Dv"))
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    rn = lambda *s: torch.randn(s, generator=gen, device=dev, dtype=torch.float32)
+    q = rn(B, T, Hk, Dk)
+    k = rn(B, T, Hk, Dk)
+    q = (q / q.pow(2).mean(-1, keepdim=True).sqrt() / Dk).to(torch.bfloat16)
+    k = (k / k.pow(2).mean(-1, keepdim=True).sqrt() / math.sqrt(Dk)).to(torch.bfloat16)
+    v = rn(B, T, Hv, Dv).to(torch.bfloat16)
+    g = torch.exp(-0.35 * torch.rand((B, T, Hv), generator=gen, device=dev))
+    beta = torch.sigmoid(rn(B, T, Hv)).to(torch.bfloat16)
+    sbytes = 4 * B * Hv * Dv * Dk
+    copies = max(1, math.ceil(ROTATE_BYTES / sbytes))
+    states = [Q.Array.from_torch(rn(B, Hv, Dv, Dk) * 0.1) for _ in range(copies)]
+    yt = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+    A = Q.Array.from_torch
+    qa, ka, va, ga, ba, ya = A(q), A(k), A(v), A(g), A(beta), A(yt)
+    torch.cuda.synchronize()
+    print(f"[bench] {args.config}: {cfg['workload']}; {copies} state copies, steps={args.steps} "
+          f"warmup={args.warmup}", file=sys.stderr, flush=True)
+
+    def step(i, st):
+        s_i = states[i % copies]
+        Q.gdn_recurrence(qa, ka, va, ga, ba, s_i, y=ya, state_out=s_i, stream=st)
+
+    for i in range(args.warmup):
+        step(i, Q.Stream.torch_current())
+    torch.cuda.synchronize()
+    ms = replay_timed(step, args.steps)
+    nbytes, flops = gdn_bytes(cfg), gdn_flops(cfg)
+    achieved = nbytes / (ms / 1e3) / 1e9
+    roof = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic_from_profiles(args.config))
+    cpu = None
+    if not args.no_cpu:
+        from gdn import gdn_recurrence  # the oracle, timed on the host as the CPU baseline
+
+        f = lambda t_: t_.float().cpu().numpy()
+        Ts = min(T, 8)
+        s0 = states[0].numpy()
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            gdn_recurrence(f(q[:, :Ts]), f(k[:, :Ts]), f(v[:, :Ts]), f(g[:, :Ts]), f(beta[:, :Ts]), s0, acc="f32")
+            reps += 1
+            if time.perf_counter() - t0 > 3.0:
+                break
+        sec_step = (time.perf_counter() - t0) / (reps * Ts)
+        cpu_sec = sec_step * T
+        cpu = {"value": round(nbytes / cpu_sec / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"{reps} runs of {Ts} of the {T} steps (numpy float32, one thread of vector ops), "
+                         f"scaled to {T} steps: {cpu_sec * 1e3:.2f} ms/call"}
+    line = {
+        "metric": "GDN recurrence GB/s & % HBM peak (state + inputs + y per call)", "value": roof["achieved"],
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "us_per_call": round(ms * 1e3, 2), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 state, bf16 q/k/v/beta/y", "data": "synthetic (seeded; RMS-normalised q, k as the model feeds)",
+        "config": {"workload": cfg["workload"], "B": B, "T": T, "Hk": Hk, "Hv": Hv, "Dk": Dk, "Dv": Dv,
+                   "state_copies": copies, "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
+                   "gflops": round(flops / (ms / 1e3) / 1e9, 1), "timing": "hip graph replay"},
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,6 +288,8 @@ def main():
         return
 
     cfg = CONFIGS[args.config]
+    if cfg.get("gdn"):
+        return bench_gdn(args, cfg)
     mode, M, N, K = cfg["mode"], cfg["M"], cfg["N"], cfg["K"]
     alg = algorithmic(cfg)
     torch.cuda.set_device(0)

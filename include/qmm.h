@@ -104,6 +104,19 @@ int qmm_dequantize(qmm_array *res, qmm_array w, qmm_array scales, qmm_array bias
 int qmm_quantize(qmm_vector_array *res, qmm_array w, qmm_optional_int group_size, qmm_optional_int bits,
                  const char *mode, qmm_array global_scale, qmm_stream s);
 
+/* The gated-delta (GDN) recurrence of mlx-runner's linear-attention layers: the
+ * packed kernel gdnKernelRun launches (src/model.zig:284-319, source
+ * src/gdn_packed.metal), with the shape rules of fusedEligible (:322-329).
+ * q, k [B, T, Hk, Dk=128] and v [B, T, Hv, Dv] (Dv % 8 == 0, Hv % Hk == 0), all
+ * bfloat16 or all float32; g [B, T, Hv] float32; beta [B, T, Hv] bfloat16 or
+ * float32; state [B, Hv, Dv, Dk] float32.  Value head hv uses key head
+ * hv / (Hv / Hk).  Per step: S *= g; dlt = (v - S k) beta; S += dlt k^T; y = S q.
+ * Results: y [B, T, Hv, Dv] in y_dtype (bfloat16 RNE or float32) and the final
+ * state [B, Hv, Dv, Dk] float32.  state_out may be the state's own handle (the
+ * update is then in place).  q, k and state must be 16-byte aligned. */
+int qmm_gdn_recurrence(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_array k, qmm_array v, qmm_array g,
+                       qmm_array beta, qmm_array state, qmm_dtype y_dtype, qmm_stream s);
+
 /* silu(g) * u element-wise, with mlx-runner's per-op roundings in the arrays' dtype
  * (bfloat16 or float32): sg = sigmoid(g), sl = g * sg, h = sl * u, each rounded
  * (silu src/model.zig:405-415, mul :451-456).  g and u must have equal shapes. */

@@ -539,6 +539,63 @@ int qmm_silu_mul(qmm_array *res, qmm_array g, qmm_array u, qmm_stream s) {
   return finish(0);
 }
 
+int qmm_gdn_recurrence(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_array k, qmm_array v, qmm_array g,
+                       qmm_array beta, qmm_array state, qmm_dtype y_dtype, qmm_stream s) {
+  const char *op = "gdn_recurrence";
+  if (!y || !state_out) return finish(fail("[%s] null result pointer", op));
+  Arr *qa = (Arr *)q.ctx, *ka = (Arr *)k.ctx, *va = (Arr *)v.ctx, *ga = (Arr *)g.ctx, *ba = (Arr *)beta.ctx,
+      *sa = (Arr *)state.ctx;
+  if (!qa || !ka || !va || !ga || !ba || !sa) return finish(fail("[%s] missing input", op));
+  // shapes and dtypes of gdnKernelRun's inputs (src/model.zig:284-319) and fusedEligible (:322-329)
+  if (qa->ndim != 4 || ka->ndim != 4 || va->ndim != 4 || sa->ndim != 4)
+    return finish(fail("[%s] q, k, v and state must be 4-D", op));
+  const int B = qa->shape[0], T = qa->shape[1], Hk = qa->shape[2], Dk = qa->shape[3];
+  const int Hv = va->shape[2], Dv = va->shape[3];
+  for (int i = 0; i < 4; ++i)
+    if (ka->shape[i] != qa->shape[i]) return finish(fail("[%s] q and k shapes differ", op));
+  if (va->shape[0] != B || va->shape[1] != T) return finish(fail("[%s] v must be [B, T, Hv, Dv]", op));
+  if (ga->ndim != 3 || ga->shape[0] != B || ga->shape[1] != T || ga->shape[2] != Hv)
+    return finish(fail("[%s] g must be [B, T, Hv]", op));
+  if (ba->ndim != 3 || ba->shape[0] != B || ba->shape[1] != T || ba->shape[2] != Hv)
+    return finish(fail("[%s] beta must be [B, T, Hv]", op));
+  if (sa->shape[0] != B || sa->shape[1] != Hv || sa->shape[2] != Dv || sa->shape[3] != Dk)
+    return finish(fail("[%s] state must be [B, Hv, Dv, Dk]", op));
+  if (qa->dtype != ka->dtype || qa->dtype != va->dtype || (qa->dtype != QMM_BFLOAT16 && qa->dtype != QMM_FLOAT32))
+    return finish(fail("[%s] q, k, v must all be bfloat16 or all float32", op));
+  if (ga->dtype != QMM_FLOAT32 || sa->dtype != QMM_FLOAT32) return finish(fail("[%s] g and state must be float32", op));
+  if (ba->dtype != QMM_BFLOAT16 && ba->dtype != QMM_FLOAT32)
+    return finish(fail("[%s] beta must be bfloat16 or float32", op));
+  if (y_dtype != QMM_BFLOAT16 && y_dtype != QMM_FLOAT32) return finish(fail("[%s] y must be bfloat16 or float32", op));
+  if (Dk != 128 || Dv <= 0 || Dv % 8 != 0 || Hk <= 0 || Hv % Hk != 0)
+    return finish(fail("[%s] needs Dk = 128, Dv a multiple of 8 and Hv a multiple of Hk (got Dk %d, Dv %d, Hk %d, Hv %d)",
+                       op, Dk, Dv, Hk, Hv));
+  if ((((uintptr_t)qa->data) | ((uintptr_t)ka->data) | ((uintptr_t)sa->data)) & 15)
+    return finish(fail("[%s] q, k and state must be 16-byte aligned", op));
+  hipStream_t st = stream_of(s);
+  Arr *ya, *so;
+  if (alloc_arr(y, {B, T, Hv, Dv}, y_dtype, st, &ya)) return finish(1);
+  if (alloc_arr(state_out, {B, Hv, Dv, Dk}, QMM_FLOAT32, st, &so)) return finish(1);
+  if (((uintptr_t)so->data) & 15) return finish(fail("[%s] state_out must be 16-byte aligned", op));
+  if ((int64_t)B * Hv == 0) return finish(0);
+  if (T == 0) {  // no steps: the state passes through
+    hipError_t e = so->data == sa->data ? hipSuccess
+                                        : hipMemcpyAsync(so->data, sa->data, sa->nbytes(), hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return finish(fail_hip(e, op));
+    return finish(0);
+  }
+  GdnArgs a;
+  a.B = B, a.T = T, a.Hk = Hk, a.Hv = Hv, a.Dk = Dk, a.Dv = Dv;
+  a.in_f32 = qa->dtype == QMM_FLOAT32;
+  a.beta_f32 = ba->dtype == QMM_FLOAT32;
+  a.y_f32 = y_dtype == QMM_FLOAT32;
+  a.q = qa->data, a.k = ka->data, a.v = va->data, a.beta = ba->data;
+  a.g = (const float *)ga->data, a.state_in = (const float *)sa->data;
+  a.state_out = (float *)so->data, a.y = ya->data;
+  hipError_t e = launch_gdn(a, st);
+  if (e != hipSuccess) return finish(fail_hip(e, op));
+  return finish(0);
+}
+
 int qmm_mlp_gate_up_silu(qmm_array *res, qmm_array x, qmm_array w_gate, qmm_array s_gate, qmm_array w_up,
                          qmm_array s_up, qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
                          qmm_stream s) {

@@ -50,6 +50,19 @@ hipError_t launch_dequant(int mode, const uint8_t *w, const uint8_t *s, int64_t 
 hipError_t launch_quantize(int mode, const void *in, bool in_f32, int64_t N, int64_t K, uint32_t *wq, uint8_t *s,
                            hipStream_t st);
 
+// Gated-delta recurrence (the reference's packed GDN kernel, src/model.zig:284-319).
+struct GdnArgs {
+  int B, T, Hk, Hv, Dk, Dv;
+  bool in_f32;    // q, k, v float32 (else bfloat16)
+  bool beta_f32;  // beta float32 (else bfloat16)
+  bool y_f32;     // y float32 (else bfloat16)
+  const void *q, *k, *v, *beta;
+  const float *g, *state_in;
+  float *state_out;
+  void *y;
+};
+hipError_t launch_gdn(const GdnArgs &a, hipStream_t st);
+
 // Zero-fill `bytes` of device memory.
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st);
 

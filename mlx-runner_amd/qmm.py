@@ -122,6 +122,8 @@ _SIGS = {
     "qmm_named_linear_q": (c_int, [POINTER(qmm_array), qmm_weight_map, qmm_array, c_char_p, qmm_stream]),
     "qmm_linear": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_stream]),
     "qmm_silu_mul": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_stream]),
+    "qmm_gdn_recurrence": (c_int, [POINTER(qmm_array), POINTER(qmm_array), qmm_array, qmm_array, qmm_array,
+                                   qmm_array, qmm_array, qmm_array, c_int, qmm_stream]),
     "qmm_mlp_gate_up_silu": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_array, qmm_array, qmm_array,
                                      qmm_optional_int, qmm_optional_int, c_char_p, qmm_stream]),
     "qmm_mlp_forward_q": (c_int, [POINTER(qmm_array), qmm_weight_map, qmm_array, c_char_p, c_char_p, c_char_p,
@@ -313,6 +315,20 @@ def silu_mul(g: Array, u: Array, *, out: Array | None = None, stream: Stream | N
     s = _stream(stream)
     check(lib.qmm_silu_mul(byref(res.h), g.h, u.h, s.h), "silu_mul")
     return res
+
+
+def gdn_recurrence(q: Array, k: Array, v: Array, g: Array, beta: Array, state: Array, *, y_dtype: int = BFLOAT16,
+                   y: Array | None = None, state_out: Array | None = None,
+                   stream: Stream | None = None) -> tuple[Array, Array]:
+    """The packed gated-delta recurrence (gdnKernelRun, src/model.zig:284-319):
+    returns (y [B, T, Hv, Dv] in y_dtype, final state [B, Hv, Dv, Dk] float32).
+    Pass state_out=state to update the state in place."""
+    yr = y if y is not None else Array()
+    so = state_out if state_out is not None else Array()
+    s = _stream(stream)
+    check(lib.qmm_gdn_recurrence(byref(yr.h), byref(so.h), q.h, k.h, v.h, g.h, beta.h, state.h, y_dtype, s.h),
+          "gdn_recurrence")
+    return yr, so
 
 
 def mlp_gate_up_silu(x: Array, w_gate: Array, s_gate: Array, w_up: Array, s_up: Array, mode: str, *,
