@@ -125,7 +125,12 @@ constexpr size_t qf_lds_bytes(int M, int Q, int F, int nmat) {
 // writes silu(gate) * up with the reference's bf16 roundings.  The per-row sums
 // are the same as those of two separate NMAT = 1 launches, so fused and
 // unfused results are identical.  D: units whose weights are in flight.
-template <int MODE, int M, int Q, int NMAT, int D>
+//
+// K longer than Q slices is walked in P passes: in pass p wave q owns slice
+// p Q + q (a slice past K re-reads the last slice and its sums are replaced by
+// zero), re-splits x for it and adds its partial sums to those of earlier
+// passes; the partials of every row block stay in LDS until the last pass.
+template <int MODE, int M, int Q, int NMAT, int D, int P>
 __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__restrict__ x,
                                                           const uint8_t *__restrict__ w,
                                                           const uint8_t *__restrict__ s, const uint8_t *__restrict__ w2,
@@ -139,29 +144,38 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   const int r_begin = (int)((int64_t)N * blockIdx.x / gridDim.x);
   const int r_end = (int)((int64_t)N * (blockIdx.x + 1) / gridDim.x);
   const int nrb = (r_end - r_begin + 15) >> 4;
-  const int k0 = 512 * q;  // this wave's K slice
+  const int S = K >> 9;  // 512-element slices
+  auto slice_of = [&](int p) __attribute__((always_inline)) {
+    const int sl = p * Q + q;
+    return sl < S ? sl : S - 1;
+  };
+  const int upp = nrb * NMAT;               // units per pass
+  const int uppd = (upp + D - 1) / D * D;   // ... rounded up to whole buffer groups
 
-  // 1) x of the slice: lane l holds elements [8l, 8l+8) of each row m
-  uint4 xr[M];
+  // 1) x of this wave's slices, all passes: lane l holds elements [8l, 8l+8) of each row m
+  uint4 xr[P][M];
 #pragma unroll
-  for (int m = 0; m < M; ++m) xr[m] = *(const uint4 *)(x + (int64_t)m * K + k0 + 8 * lane);
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int m = 0; m < M; ++m) xr[p][m] = *(const uint4 *)(x + (int64_t)m * K + 512 * slice_of(p) + 8 * lane);
 
   // 2) the first unit's weights.  Load i, lane l: nvfp4 row 4i + l/16, bytes 16 (l%16);
   //    mxfp8 row 2i + l/32, bytes 16 (l%32).  Scales: lane l, row l/4, bytes (l%4) SB/4.
   constexpr int RPL = MODE == NVFP4 ? 4 : 2;  // rows per load
   constexpr int LPR = 64 / RPL;               // lanes per row
   const int64_t wrow = MODE == NVFP4 ? (K >> 1) : K, srow = MODE == NVFP4 ? (K >> 4) : (K >> 5);
-  const int wcol = q * G::UB + 16 * (lane % LPR);
-  const int scol = q * G::SB + (lane & 3) * (G::SB / 4);
   auto row_of = [&](int rb, int rr) __attribute__((always_inline)) {
     const int row = r_begin + 16 * rb + rr;
     return row < r_end ? row : r_end - 1;  // rows past the range re-read its last row (results dropped)
   };
-  // unit u = (row block u / NMAT, matrix u % NMAT) lives in buffer u % D
+  // unit u = (pass u / uppd, row block (u % uppd) / NMAT, matrix u % NMAT) lives in buffer
+  // u % D; units past a pass's last row block load clamped rows and are not stored
   uint4 wv[D][G::LOADS];
   uint32_t sv0[D], sv1[D];
   auto load_unit = [&](int u, int buf) __attribute__((always_inline)) {
-    const int rb = u / NMAT, mat = u % NMAT;
+    const int pass = u / uppd, r = u - pass * uppd, rb = r / NMAT, mat = r - rb * NMAT;
+    const int sl = slice_of(pass < P ? pass : P - 1);
+    const int wcol = sl * G::UB + 16 * (lane % LPR), scol = sl * G::SB + (lane & 3) * (G::SB / 4);
     const uint8_t *wm = mat ? w2 : w, *sm = mat ? s2 : s;
 #pragma unroll
     for (int i = 0; i < G::LOADS; ++i)
@@ -179,15 +193,20 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   load_unit(0, 0);
 
   // 3) x split into records in this wave's tile (before it holds weights), then the
-  //    A operands of the slice's 4 chunks into registers, kept for the whole kernel.
+  //    A operands of the slice's 4 chunks into registers, kept for the pass.
+  //    E4M3 A layout: lane group h, byte t holds logical K 64 (t/16) + 16 h + t%16.
   uint8_t *ex = tile + 4 * 4 * QF_REC;  // exponent bytes, 64 per x row
-  {
+  const int h = lane >> 4, n = lane & 15;
+  constexpr int MA = MODE == NVFP4 ? M : 1;  // A operands per chunk
+  i32x8_t areg[4][MA];
+  int asreg[4][MA];
+  auto prep = [&](const uint4(&xin)[M]) __attribute__((always_inline)) {
     const int c = lane >> 4, kc = (lane & 15) * 8;  // chunk of the slice, offset in the chunk
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       uint2 hi, lo;
       int th, tl;
-      split8<MODE == NVFP4 ? 2 : 4>(xr[m], hi, lo, th, tl);
+      split8<MODE == NVFP4 ? 2 : 4>(xin[m], hi, lo, th, tl);
       uint8_t *rec = tile + (m * 4 + c) * QF_REC;
       if constexpr (MODE == NVFP4) {
         // group g of the chunk: hi at 32 g, lo at 32 g + 16; exponents [m][g][hl][c]
@@ -209,21 +228,11 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
       }
     }
     if (lane < 4 * M) *(uint4 *)(tile + lane * QF_REC + 256) = make_uint4(0, 0, 0, 0);
-  }
-#pragma unroll
-  for (int d = 1; d < D; ++d) load_unit(d, d);
-  // A-operand addressing of this lane (row n = lane % 16 of the A operand).
-  //   E4M3 A layout: lane group h, byte t holds logical K 64 (t/16) + 16 h + t%16.
-  const int h = lane >> 4, n = lane & 15;
-  constexpr int MA = MODE == NVFP4 ? M : 1;  // A operands per chunk
-  i32x8_t areg[4][MA];
-  int asreg[4][MA];
-  {
     int aoff0, aoff1, am, ebase;
     if constexpr (MODE == NVFP4) {
       // column n = 4p + v: group g = 2p + v/2 of the chunk, hi (v even) or lo; nonzero only
       // where logical K is in group g, i.e. lane group g%4, byte half g/4
-      const int p = n >> 2, v = n & 3, g = 2 * p + (v >> 1), hl = v & 1;
+      const int pp = n >> 2, v = n & 3, g = 2 * pp + (v >> 1), hl = v & 1;
       const bool own = h == (g & 3);
       aoff0 = own && g < 4 ? 32 * g + 16 * hl : 256;
       aoff1 = own && g >= 4 ? 32 * g + 16 * hl : 256;
@@ -232,22 +241,25 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
     } else {
       // column n = 2m + hl for m < M; the other columns are zero
       const int m = n >> 1, hl = n & 1;
-      const bool live = m < M;
-      aoff0 = live ? 128 * hl + 16 * h : 256;
-      aoff1 = live ? 128 * hl + 64 + 16 * h : 256;
-      am = live ? m : 0;
+      const bool lv = m < M;
+      aoff0 = lv ? 128 * hl + 16 * h : 256;
+      aoff1 = lv ? 128 * hl + 64 + 16 * h : 256;
+      am = lv ? m : 0;
       ebase = am * 64 + hl * 16 + h;  // + 4c: block h of chunk c
     }
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
       for (int m = 0; m < MA; ++m) {
-        const uint8_t *rec = tile + ((MODE == NVFP4 ? m : am) * 4 + c) * QF_REC;
+        const uint8_t *rec = tile + ((MODE == NVFP4 ? m : am) * 4 + cc) * QF_REC;
         const uint4 u0 = *(const uint4 *)(rec + aoff0), u1 = *(const uint4 *)(rec + aoff1);
-        areg[c][m] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
-        asreg[c][m] = MODE == NVFP4 ? ex[m * 64 + ebase + c] : ex[ebase + 4 * c];
+        areg[cc][m] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+        asreg[cc][m] = MODE == NVFP4 ? ex[m * 64 + ebase + cc] : ex[ebase + 4 * cc];
       }
-  }
+  };
+  prep(xr[0]);
+#pragma unroll
+  for (int d = 1; d < D; ++d) load_unit(d, d);
 
   // sum the waves' partials of row blocks [rb_first, rb_last] in wave order
   auto flush = [&](int rb_first, int rb_last) __attribute__((always_inline)) {
@@ -271,14 +283,16 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   };
 
   uint8_t *wt = tile, *st = tile + 16 * G::PITCH;
-  const int units = nrb * NMAT;
-  // units go in groups of D so that buffer indices are static; the units past
-  // the last one are computed too (clamped rows): loads and MFMAs under a branch
-  // make the compiler's wait counting conservative.
-  for (int u0 = 0; u0 < units; u0 += D) {
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+   if (p > 0) prep(xr[p]);
+   // units go in groups of D so that buffer indices are static; the units past
+   // the last one are computed too (clamped rows): loads and MFMAs under a branch
+   // make the compiler's wait counting conservative.
+   for (int r0 = 0; r0 < uppd; r0 += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      const int u = u0 + d, rb = u / NMAT, mat = u % NMAT;
+      const int r = r0 + d, rb = r / NMAT, mat = r - rb * NMAT;
       // unit u: registers -> tile (the x records are no longer needed there), then refill
       // the buffer with unit u + D (past the last unit: clamped rows, unused)
 #pragma unroll
@@ -288,8 +302,10 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
         *(uint2 *)(st + 8 * lane) = make_uint2(sv0[d], sv1[d]);
       else
         *(uint32_t *)(st + 4 * lane) = sv0[d];
-      load_unit(u + D, d);
-      const bool live = u < units;
+      load_unit(p * uppd + r + D, d);
+      const bool live = r < upp;
+      // a slice past K (last pass only) re-read the last slice: its sums are dropped
+      const bool real = P == 1 || p * Q + q < S;
       const int rbf = rb % F;
       float *pslot = part + ((rbf * NMAT + mat) * M) * Q * 16;
       if constexpr (MODE == NVFP4) {
@@ -317,7 +333,11 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
           float a = acc[m];
           a += __shfl_xor(a, 16);
           a += __shfl_xor(a, 32);
-          if (live && h == 0) pslot[(m * Q + q) * 16 + n] = a;
+          if (live && h == 0) {
+            float *dst = pslot + (m * Q + q) * 16 + n;
+            a = real ? a : 0.f;
+            *dst = p == 0 ? a : *dst + a;
+          }
         }
       } else {
         f32x4_t dd = {0.f, 0.f, 0.f, 0.f};
@@ -336,31 +356,67 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
 #pragma unroll
         for (int v2 = 0; v2 < 2; ++v2) {
           const int m = 2 * h + v2;
-          if (live && m < M) pslot[(m * Q + q) * 16 + n] = dd[2 * v2] + dd[2 * v2 + 1];
+          if (live && m < M) {
+            float *dst = pslot + (m * Q + q) * 16 + n;
+            const float a = real ? dd[2 * v2] + dd[2 * v2 + 1] : 0.f;
+            *dst = p == 0 ? a : *dst + a;
+          }
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) keep_live(bsc[c]);
       }
-      if (live && mat == NMAT - 1 && ((rb + 1) % F == 0 || rb + 1 == nrb)) flush(rb - rbf, rb);
+      // with several passes the host sets F >= nrb: one flush, after the last pass
+      if (live && p == P - 1 && mat == NMAT - 1 && ((rb + 1) % F == 0 || rb + 1 == nrb)) flush(rb - rbf, rb);
     }
+   }
   }
 }
 
 }  // namespace
 
-// Waves per workgroup for K: one per 512-element slice.
-static int qf_waves(int K) { return (K > 0 && K % 512 == 0 && K / 512 <= 16) ? K / 512 : 0; }
+// Waves per workgroup (Q) and passes (P) for K: the decode shapes served are
+// K = 5120 (10 slices of 512: Q = 10, P = 1) and K = 17408 (34 slices: Q = 12,
+// P = 3, two slices of the last pass past K).
+struct QfShape {
+  int Q, P;
+};
+static QfShape qf_shape(int K) {
+  if (K == 5120) return {10, 1};
+  if (K == 17408) return {12, 3};
+  return {0, 0};
+}
+
+static int qf_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      cus = n;
+  }
+  return cus;
+}
+
+static int qf_nrb(const QmmArgs &a, int cus) {
+  const int rbs = (a.N + 15) / 16;
+  const int grid = rbs < cus ? rbs : cus;
+  return ((a.N + grid - 1) / grid + 15) / 16;
+}
 
 bool qmv_mfma_ok(const QmmArgs &a) {
   if (a.x_f32 || a.M < 1 || a.N < 16) return false;
   if (a.M > (a.mode == NVFP4 ? 2 : 4)) return false;  // nvfp4 M = 3, 4 would not fit the A operands in registers
-  if (qf_waves(a.K) != 10) return false;              // instantiated for K = 5120
+  const QfShape g = qf_shape(a.K);
+  if (g.Q == 0) return false;
   // Where this path is faster than the unpacking GEMV (measured on the 256-CU
-  // MI355X, K = 5120): at M = 1 only for nvfp4 with many rows per CU (it pays a
-  // per-workgroup x split and pipeline fill; mxfp8 decodes at 1 VALU op per
-  // weight byte and streams at HBM speed either way), at M >= 2 from N = 4096.
-  if (a.M == 1 && (a.mode != NVFP4 || a.N < 16384)) return false;
+  // MI355X): at M = 1 only for nvfp4, with many rows per CU at K = 5120 (it pays
+  // a per-workgroup x split and pipeline fill) and at K = 17408 (N = 5120: 11.8
+  // against 12.4 us); mxfp8 at M = 1 decodes at 1 VALU op per weight byte and
+  // streams faster through the unpacking GEMV (K = 17408: 17.2 against 19.8 us).
+  // At M >= 2 from N = 4096.
+  if (a.M == 1 && (a.mode != NVFP4 || (g.P == 1 && a.N < 16384))) return false;
   if (a.N < 4096) return false;
+  // several passes keep every row block's partial sums in LDS
+  if (g.P > 1 && (qf_cus() == 0 || qf_nrb(a, qf_cus()) > QF_FLUSH_MAX)) return false;
   if ((((uintptr_t)a.x) | ((uintptr_t)a.w)) & 15) return false;
   if (((uintptr_t)a.s) & 7) return false;  // scale slices are read as 8 (nvfp4) / 4 (mxfp8) bytes
   return true;
@@ -370,11 +426,10 @@ bool qmv_mfma_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up)
   return qmv_mfma_ok(a) && (((uintptr_t)w_up) & 15) == 0 && (((uintptr_t)s_up) & 7) == 0;
 }
 
-template <int MODE, int M, int NMAT, int D>
+template <int MODE, int M, int Q, int NMAT, int D, int P>
 static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
                             hipStream_t st) {
-  constexpr int Q = 10;
-  auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D>;
+  auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D, P>;
   const size_t lds = qf_lds_bytes<MODE>(M, Q, F, NMAT);
   static bool attr_set = false;
   if (!attr_set) {
@@ -389,26 +444,25 @@ static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *
 
 // Two units in flight per wave when each workgroup has few row blocks (the call
 // is then a few memory latencies long); one otherwise, which streams faster.
+// K = 17408 (three passes, no MLP form) keeps one unit in flight: x of all
+// passes is held in registers.
 template <int MODE, int M, int NMAT>
 static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F, int nrb,
                               hipStream_t st) {
-  if (nrb * NMAT <= 4) return launch_qf<MODE, M, NMAT, 2>(a, w2, s2, grid, F, st);
-  return launch_qf<MODE, M, NMAT, 1>(a, w2, s2, grid, F, st);
+  if constexpr (NMAT == 1)
+    if (qf_shape(a.K).P == 3) return launch_qf<MODE, M, 12, 1, 1, 3>(a, w2, s2, grid, F, st);
+  if (nrb * NMAT <= 4) return launch_qf<MODE, M, 10, NMAT, 2, 1>(a, w2, s2, grid, F, st);
+  return launch_qf<MODE, M, 10, NMAT, 1, 1>(a, w2, s2, grid, F, st);
 }
 
 template <int NMAT>
 static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, hipStream_t st) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return e;
-  }
+  const int cus = qf_cus();
+  if (cus == 0) return hipErrorNoDevice;
   const int rbs = (a.N + 15) / 16;
   const int grid = rbs < cus ? rbs : cus;
-  const int rows_max = (a.N + grid - 1) / grid;
-  const int nrb = (rows_max + 15) / 16;
+  const int nrb = qf_nrb(a, cus);
+  if (qf_shape(a.K).P > 1 && nrb > QF_FLUSH_MAX) return hipErrorInvalidValue;
   const int F = nrb < QF_FLUSH_MAX ? nrb : QF_FLUSH_MAX;
   if (a.mode == NVFP4) {
     if (a.M == 1) return launch_qf_d<NVFP4, 1, NMAT>(a, w2, s2, grid, F, nrb, st);

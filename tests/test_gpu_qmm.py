@@ -367,6 +367,28 @@ def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
     assert np.array_equal(run_qmm(mode, xb, wq, s), y)
 
 
+# K = 17408 (the MLP down projection): 34 slices of 512 walked by 12 waves in 3
+# passes, the last pass with 2 slices past K.  The edge groups are planted in
+# the first slice of every pass and in the last slice.
+@pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 5120), ("nvfp4", 2, 4099), ("mxfp8", 2, 5120),
+                                      ("mxfp8", 3, 4101), ("mxfp8", 4, 8192)])
+@pytest.mark.parametrize("xkind", ["normal", "edge"])
+def test_decode_mfma_down_shapes_match_oracle(mode, M, N, xkind):
+    K = 17408
+    rng = np.random.default_rng(N * 10 + M + 1)
+    wq, s = rand_packed(rng, mode, N, K)
+    xb = make_x(rng, M, K, xkind)
+    if xkind == "edge":
+        for off in (12 * 512, 24 * 512, K - 512):
+            xb[:, off:off + 128] = xb[:, 0:128]
+    y = run_qmm(mode, xb, wq, s)
+    cols = np.unique(np.concatenate([np.arange(0, N, 11), np.arange(N - 40, N), np.arange(40)]))
+    ref = O.qmm(mode, xb, wq, s, cols=cols)
+    ok, fro, worst = O.check_tolerance(f32(y[:, cols]), f32(ref), **TOL)
+    assert ok, (fro, worst)
+    assert np.array_equal(run_qmm(mode, xb, wq, s), y)
+
+
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 2, 4099), ("mxfp8", 3, 4101)])
 def test_mlp_gate_up_silu_mfma_shapes(mode, M, N):
     """The fused MLP on the MFMA path: equal to two quantized_matmul + silu_mul bit for
