@@ -1,9 +1,10 @@
-// Decode GEMV on the gfx950 scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4):
-// y[m, n] = sum_k x[m, k] * deq(W)[n, k] for M = 1..4, bf16 x, K = 512 * Q.
+// Decode GEMV on the gfx950 scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4, and
+// the 32x32x64 form for nvfp4 at M = 3-4): y[m, n] = sum_k x[m, k] * deq(W)[n, k]
+// for M = 1..4, bf16 x, K = 5120 or 17408.
 //
-// The shapes are mlx-runner's per-token qmm calls with K = 5120
-// (src/model.zig:906-908 gate/up, :929-944 q/k/v, :1066-1074, :1309 lm_head;
-// M = 1 decode, 2-3 MTP verify).  They are HBM-bound.  This path moves the
+// The shapes are mlx-runner's per-token qmm calls (src/model.zig:906-908
+// gate/up and :912 down, :929-944 q/k/v, :1066-1074, :1309 lm_head; M = 1
+// decode, 2-4 MTP verify).  They are HBM-bound.  This path moves the
 // per-element decode work off the VALU so that it no longer competes with the
 // weight stream:
 //
@@ -30,11 +31,11 @@
 // Work split: one workgroup per CU owns a contiguous range of rows (N spread
 // evenly, so every CU reads the same number of HBM bytes).  Wave q owns the K
 // slice [512q, 512q + 512) and keeps the A operands of its 4 chunks in
-// registers for the whole kernel; the waves walk the range's 16-row blocks in
-// step.  Per row block a wave loads its slice with contiguous 1 KiB loads,
-// passes it through a private LDS tile into the MFMA layout, and writes 16
-// partial sums to LDS; the partials are summed over the waves in a fixed
-// order, so the result is deterministic.
+// registers; the waves walk the range's 16-row blocks in step.  K = 17408
+// (34 slices) is walked by 12 waves in 3 passes.  Per row block a wave loads
+// its slice with contiguous loads, passes it through a private LDS tile into
+// the MFMA layout, and writes 16 partial sums to LDS; the partials are summed
+// over the waves in a fixed order, so the result is deterministic.
 #include "qmm_device.h"
 #include "qmm_launch.h"
 
@@ -95,6 +96,44 @@ __device__ __forceinline__ void split8(const uint4 q, uint2 &hi, uint2 &lo, int 
   }
   hi = make_uint2(hw[0], hw[1]);
   lo = make_uint2(lw[0], lw[1]);
+}
+
+// x of one 512-element slice, split into E4M3 hi/lo records in a wave's LDS tile.
+// Lane l holds elements [8l, 8l+8) of each x row m.  Record (m, c) of 128-element
+// chunk c sits at tile + (m * 4 + c) * QF_REC and ends in 16 zero bytes; the
+// exponent bytes (E8M0 codes) follow the records, 64 per x row.
+//   nvfp4: group g (16 elements) of the chunk: hi at 32 g, lo at 32 g + 16;
+//          exponent of (m, g, hi|lo, c) at 64 m + (2 g + hl) * 4 + c.
+//   mxfp8: hi at [0, 128), lo at [128, 256) in K order; exponent of
+//          (m, hi|lo, c, block) at 64 m + (4 hl + c) * 4 + block.
+template <int MODE, int M>
+__device__ __forceinline__ void qf_write_records(uint8_t *tile, const uint4 (&xin)[M], int lane) {
+  uint8_t *ex = tile + 4 * 4 * QF_REC;
+  const int c = lane >> 4, kc = (lane & 15) * 8;  // chunk of the slice, offset in the chunk
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    uint2 hi, lo;
+    int th, tl;
+    split8<MODE == NVFP4 ? 2 : 4>(xin[m], hi, lo, th, tl);
+    uint8_t *rec = tile + (m * 4 + c) * QF_REC;
+    if constexpr (MODE == NVFP4) {
+      const int g = kc >> 4, half = (kc >> 3) & 1;
+      *(uint2 *)(rec + 32 * g + 8 * half) = hi;
+      *(uint2 *)(rec + 32 * g + 16 + 8 * half) = lo;
+      if (half == 0) {
+        ex[m * 64 + (g * 2 + 0) * 4 + c] = (uint8_t)(th + 127);
+        ex[m * 64 + (g * 2 + 1) * 4 + c] = (uint8_t)(tl + 127);
+      }
+    } else {
+      *(uint2 *)(rec + kc) = hi;
+      *(uint2 *)(rec + 128 + kc) = lo;
+      if ((kc & 31) == 0) {
+        ex[m * 64 + (0 * 4 + c) * 4 + (kc >> 5)] = (uint8_t)(th + 127);
+        ex[m * 64 + (1 * 4 + c) * 4 + (kc >> 5)] = (uint8_t)(tl + 127);
+      }
+    }
+  }
+  if (lane < 4 * M) *(uint4 *)(tile + lane * QF_REC + 256) = make_uint4(0, 0, 0, 0);
 }
 
 // A unit is one wave's K slice (512 elements = 4 chunks of 128) of one 16-row block:
@@ -201,33 +240,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   i32x8_t areg[4][MA];
   int asreg[4][MA];
   auto prep = [&](const uint4(&xin)[M]) __attribute__((always_inline)) {
-    const int c = lane >> 4, kc = (lane & 15) * 8;  // chunk of the slice, offset in the chunk
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      uint2 hi, lo;
-      int th, tl;
-      split8<MODE == NVFP4 ? 2 : 4>(xin[m], hi, lo, th, tl);
-      uint8_t *rec = tile + (m * 4 + c) * QF_REC;
-      if constexpr (MODE == NVFP4) {
-        // group g of the chunk: hi at 32 g, lo at 32 g + 16; exponents [m][g][hl][c]
-        const int g = kc >> 4, half = (kc >> 3) & 1;
-        *(uint2 *)(rec + 32 * g + 8 * half) = hi;
-        *(uint2 *)(rec + 32 * g + 16 + 8 * half) = lo;
-        if (half == 0) {
-          ex[m * 64 + (g * 2 + 0) * 4 + c] = (uint8_t)(th + 127);
-          ex[m * 64 + (g * 2 + 1) * 4 + c] = (uint8_t)(tl + 127);
-        }
-      } else {
-        // hi at [0, 128), lo at [128, 256) in K order; exponents [m][hl][c][block]
-        *(uint2 *)(rec + kc) = hi;
-        *(uint2 *)(rec + 128 + kc) = lo;
-        if ((kc & 31) == 0) {
-          ex[m * 64 + (0 * 4 + c) * 4 + (kc >> 5)] = (uint8_t)(th + 127);
-          ex[m * 64 + (1 * 4 + c) * 4 + (kc >> 5)] = (uint8_t)(tl + 127);
-        }
-      }
-    }
-    if (lane < 4 * M) *(uint4 *)(tile + lane * QF_REC + 256) = make_uint4(0, 0, 0, 0);
+    qf_write_records<MODE, M>(tile, xin, lane);
     int aoff0, aoff1, am, ebase;
     if constexpr (MODE == NVFP4) {
       // column n = 4p + v: group g = 2p + v/2 of the chunk, hi (v even) or lo; nonzero only
@@ -372,6 +385,171 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   }
 }
 
+// nvfp4 at M = 3-4 (MTP verify): the 16x16x128 form needs one A operand per x
+// row (16 columns = 8 groups x hi|lo), too many registers past M = 2.  The
+// 32x32x64 MFMA has 32 A rows per 64-element chunk, room for 4 x rows x 4
+// groups x hi|lo, so one A operand per chunk serves all rows:
+//   A row i = 8 m + 2 g + hl holds x row m's hi (hl = 0) or lo part on group g
+//   of the chunk and zero elsewhere.  Lane (i, h) of the E4M3 operand holds K
+//   16 h + [0,16) in bytes 0-15 and 32 + 16 h + [0,16) in bytes 16-31 (measured),
+//   so it carries the group's 16 bytes in one half when g = h or g = 2 + h.
+//   Its block scale covers block h = K [32h, 32h+32) of row i.
+//   B lane (j, h) holds E2M1 K [32 h, 32 h + 32) of weight row j: 16 bytes of it.
+//   Output lane (j, h), element v: A row 8 (v / 4) + 4 h + v % 4, i.e. x row
+//   m = v / 4, group 2 h + (v % 4) / 2, hi|lo = v % 2; the E4M3 scales of
+//   groups 2h, 2h+1 of row j weight them in fp32.
+// Units are 32 rows x one 512-element slice (8 KiB of E2M1, 8 loads of 1 KiB),
+// staged through the wave's LDS tile as in qmv_mfma_kernel.  K longer than Q
+// slices is walked in P passes (slice p Q + q in pass p); x of the next pass
+// is loaded when a pass starts, so one pass of x is held in registers.
+constexpr int Q32_PITCH = 272;                       // tile row pitch (256 bytes + 16)
+constexpr int Q32_TILE = 32 * Q32_PITCH + 32 * 32;   // 32 rows of weights + their 32 scale bytes
+constexpr int Q32_WAVE_LDS = Q32_TILE > 4 * 4 * QF_REC + 4 * 64 ? Q32_TILE : 4 * 4 * QF_REC + 4 * 64;
+
+constexpr int Q32_FLUSH_MAX = 4;
+constexpr size_t q32_lds_bytes(int M, int Q, int F) { return (size_t)Q * Q32_WAVE_LDS + (size_t)F * M * Q * 64 * 4; }
+
+template <int M, int Q, int P>
+__global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__restrict__ x,
+                                                            const uint8_t *__restrict__ w,
+                                                            const uint8_t *__restrict__ s, uint16_t *__restrict__ y,
+                                                            int N, int K, int F) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
+  uint8_t *tile = lds + q * Q32_WAVE_LDS;
+  float *part = (float *)(lds + Q * Q32_WAVE_LDS);  // [F][M][Q][2][32] partial sums (wave, lane half)
+  const int r_begin = (int)((int64_t)N * blockIdx.x / gridDim.x);
+  const int r_end = (int)((int64_t)N * (blockIdx.x + 1) / gridDim.x);
+  const int nrb = (r_end - r_begin + 31) >> 5;
+  const int S = K >> 9;
+  auto slice_of = [&](int p) __attribute__((always_inline)) {
+    const int sl = p * Q + q;
+    return sl < S ? sl : S - 1;
+  };
+
+  uint4 xr[M];
+  auto load_x = [&](int p) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) xr[m] = *(const uint4 *)(x + (int64_t)m * K + 512 * slice_of(p) + 8 * lane);
+  };
+  load_x(0);
+
+  // unit u = (pass u / nrb, row block u % nrb).  Load i, lane l: row 4i + l/16,
+  // bytes 16 (l%16) of the slice; scales: lane l, row l/2, bytes 16 (l%2).
+  const int64_t wrow = K >> 1, srow = K >> 4;
+  auto row_of = [&](int rb, int rr) __attribute__((always_inline)) {
+    const int row = r_begin + 32 * rb + rr;
+    return row < r_end ? row : r_end - 1;  // rows past the range re-read its last row (results dropped)
+  };
+  uint4 wv[8], sv;
+  auto load_unit = [&](int u) __attribute__((always_inline)) {
+    const int pass = u / nrb, rb = u - pass * nrb;
+    const int sl = slice_of(pass < P ? pass : P - 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      wv[i] = load_stream16(w + row_of(rb, 4 * i + (lane >> 4)) * wrow + sl * 256 + 16 * (lane & 15));
+    sv = *(const uint4 *)(s + row_of(rb, lane >> 1) * srow + sl * 32 + 16 * (lane & 1));
+  };
+  load_unit(0);
+
+  // A operands of the slice's 8 chunks (see above), from the x records
+  const int i = lane & 31, h = lane >> 5;
+  const int am = i >> 3, ag = (i >> 1) & 3, ahl = i & 1;
+  const bool alive = am < M, own0 = alive && ag == h, own1 = alive && ag == 2 + h;
+  // A lane (i, h) is nonzero in bytes 0-15 (own0) or 16-31 (own1) or nowhere, the
+  // same half for every chunk: only those 16 bytes are kept, the operand is
+  // rebuilt with masks at each MFMA
+  const uint32_t amask0 = own0 ? 0xFFFFFFFFu : 0u, amask1 = own1 ? 0xFFFFFFFFu : 0u;
+  const int aoff = 32 * ag + 16 * ahl;  // in record (m, c8 / 2), + 128 for odd c8
+  const int arec = (alive ? am : 0) * 4, aex = 4 * 4 * QF_REC + (alive ? am : 0) * 64 + (ag * 2 + ahl) * 4;
+  uint4 areg[8];
+  int asreg[8];
+  auto prep = [&]() __attribute__((always_inline)) {
+    qf_write_records<NVFP4, M>(tile, xr, lane);
+#pragma unroll
+    for (int c8 = 0; c8 < 8; ++c8) {
+      // 64-element chunk c8 = half c8 % 2 of 128-element record c8 / 2: groups 4 (c8 % 2) + [0, 4)
+      areg[c8] = *(const uint4 *)(tile + (arec + (c8 >> 1)) * QF_REC + 128 * (c8 & 1) + aoff);
+      asreg[c8] = tile[aex + 4 * 8 * (c8 & 1) + (c8 >> 1)];
+    }
+  };
+
+  auto flush = [&](int rb_first, int rb_last) __attribute__((always_inline)) {
+    lds_barrier();
+    const int items = (rb_last - rb_first + 1) * M * 32;
+    for (int t = tid; t < items; t += 64 * Q) {
+      const int nn = t & 31, m = (t >> 5) % M, rbi = (t >> 5) / M;
+      const int rb = rb_first + rbi, row = r_begin + 32 * rb + nn;
+      const float *pp = part + (((rb % F) * M + m) * Q) * 64 + nn;
+      float sum = 0.f;
+#pragma unroll
+      for (int qh = 0; qh < 2 * Q; ++qh) sum += pp[32 * qh];
+      if (row < r_end) y[(int64_t)m * N + row] = f32_to_bf16_rne(sum);
+    }
+    lds_barrier();
+  };
+
+  uint8_t *wt = tile, *st = tile + 32 * Q32_PITCH;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    prep();
+    if (p + 1 < P) load_x(p + 1);
+    // a slice past K (last pass only) re-read the last slice: its sums are dropped
+    const bool real = P == 1 || p * Q + q < S;
+    // a do-while: every workgroup has a row block, and the compiler then counts the
+    // next pass's x loads as older than the unit loads (exact wait before the split)
+    int rb = 0;
+    do {
+      // unit (p, rb): registers -> tile (the x records are no longer needed there), then
+      // refill the registers with the next unit (past the last one: clamped, unused)
+#pragma unroll
+      for (int li = 0; li < 8; ++li) *(uint4 *)(wt + (4 * li + (lane >> 4)) * Q32_PITCH + 16 * (lane & 15)) = wv[li];
+      *(uint4 *)(st + 16 * lane) = sv;
+      load_unit(p * nrb + rb + 1);
+      float acc[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[m] = 0.f;
+#pragma unroll
+      for (int c8 = 0; c8 < 8; ++c8) {
+        const uint4 b = *(const uint4 *)(wt + i * Q32_PITCH + 32 * c8 + 16 * h);
+        // the MFMA of chunk c8 waits for the sums of chunk c8 - 1: issued any earlier,
+        // the chunks' 16 output registers would all be live at once
+        int b0 = (int)b.x;
+#pragma unroll
+        for (int m = 0; m < M; ++m) asm volatile("" : "+v"(b0) : "v"(acc[m]));
+        const i32x8_t bw = {b0, (int)b.y, (int)b.z, (int)b.w, 0, 0, 0, 0};
+        const f32x2_t sc = __builtin_amdgcn_cvt_pk_f32_fp8((int)*(const uint16_t *)(st + i * 32 + 4 * c8 + 2 * h), false);
+        // (the masks pass through asm so that the masked operands are not hoisted out of
+        // the loop as invariants: that would hold all 8 full operands in registers)
+        uint32_t k0 = amask0, k1 = amask1;
+        asm volatile("" : "+v"(k0), "+v"(k1));
+        const uint4 ad = areg[c8];
+        const i32x8_t aw = {(int)(ad.x & k0), (int)(ad.y & k0), (int)(ad.z & k0), (int)(ad.w & k0),
+                            (int)(ad.x & k1), (int)(ad.y & k1), (int)(ad.z & k1), (int)(ad.w & k1)};
+        const f32x16_t dd = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            aw, bw, f32x16_t{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, 0, 4,
+            0, asreg[c8], 0, 127);
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+          acc[m] += sc.x * (dd[4 * m] + dd[4 * m + 1]) + sc.y * (dd[4 * m + 2] + dd[4 * m + 3]);
+      }
+      // every lane stores its half's sums (no branch: the compiler would sink the
+      // accumulation of rows m > 0 into it and keep all chunks' outputs live)
+      const int rbf = rb % F;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float *dst = part + ((rbf * M + m) * Q + q) * 64 + lane;
+        const float a = real ? acc[m] : 0.f;
+        *dst = p == 0 ? a : *dst + a;
+      }
+#pragma unroll
+      for (int c8 = 0; c8 < 8; ++c8) keep_live(asreg[c8]);
+      // with several passes the host sets F >= nrb: one flush, after the last pass
+      if (p == P - 1 && ((rb + 1) % F == 0 || rb + 1 == nrb)) flush(rb - rbf, rb);
+    } while (++rb < nrb);
+  }
+}
+
 }  // namespace
 
 // Waves per workgroup (Q) and passes (P) for K: the decode shapes served are
@@ -402,9 +580,27 @@ static int qf_nrb(const QmmArgs &a, int cus) {
   return ((a.N + grid - 1) / grid + 15) / 16;
 }
 
+constexpr size_t QF_LDS_MAX = 160 * 1024;
+
+// Row blocks per partial-sum flush: up to QF_FLUSH_MAX, as many as fit the LDS.
+static int qf_flush_rows(const QmmArgs &a, int nmat, int nrb) {
+  const QfShape g = qf_shape(a.K);
+  int F = nrb < QF_FLUSH_MAX ? nrb : QF_FLUSH_MAX;
+  while (F > 1 && (a.mode == NVFP4 ? qf_lds_bytes<NVFP4>(a.M, g.Q, F, nmat) : qf_lds_bytes<MXFP8>(a.M, g.Q, F, nmat)) >
+                      QF_LDS_MAX)
+    --F;
+  return F;
+}
+
+static bool q32_ok(const QmmArgs &a);
+
 bool qmv_mfma_ok(const QmmArgs &a) {
-  if (a.x_f32 || a.M < 1 || a.N < 16) return false;
-  if (a.M > (a.mode == NVFP4 ? 2 : 4)) return false;  // nvfp4 M = 3, 4 would not fit the A operands in registers
+  if (a.x_f32 || a.M < 1 || a.N < 16 || a.M > 4) return false;
+  // nvfp4 at M = 3-4 runs the 32x32x64 form (the 16x16x128 form's A operands would
+  // not fit in registers); measured faster than the unpacking GEMV from N = 4096
+  // (N = 5120, K = 5120, M = 3: 7.8 against 9.4 us; gate+up M = 3: 22.8 against 30.7;
+  // down M = 3: 17.1 against 22.5)
+  if (a.mode == NVFP4 && a.M > 2) return a.N >= 4096 && q32_ok(a);
   const QfShape g = qf_shape(a.K);
   if (g.Q == 0) return false;
   // Where this path is faster than the unpacking GEMV (measured on the 256-CU
@@ -416,13 +612,15 @@ bool qmv_mfma_ok(const QmmArgs &a) {
   if (a.M == 1 && (a.mode != NVFP4 || (g.P == 1 && a.N < 16384))) return false;
   if (a.N < 4096) return false;
   // several passes keep every row block's partial sums in LDS
-  if (g.P > 1 && (qf_cus() == 0 || qf_nrb(a, qf_cus()) > QF_FLUSH_MAX)) return false;
+  if (g.P > 1 && (qf_cus() == 0 || qf_flush_rows(a, 1, qf_nrb(a, qf_cus())) < qf_nrb(a, qf_cus()))) return false;
   if ((((uintptr_t)a.x) | ((uintptr_t)a.w)) & 15) return false;
   if (((uintptr_t)a.s) & 7) return false;  // scale slices are read as 8 (nvfp4) / 4 (mxfp8) bytes
   return true;
 }
 
+// The fused MLP form exists for the 16x16x128 kernel only (nvfp4 M <= 2, mxfp8 M <= 4).
 bool qmv_mfma_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up) {
+  if (a.mode == NVFP4 && a.M > 2) return false;
   return qmv_mfma_ok(a) && (((uintptr_t)w_up) & 15) == 0 && (((uintptr_t)s_up) & 7) == 0;
 }
 
@@ -462,8 +660,8 @@ static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8
   const int rbs = (a.N + 15) / 16;
   const int grid = rbs < cus ? rbs : cus;
   const int nrb = qf_nrb(a, cus);
-  if (qf_shape(a.K).P > 1 && nrb > QF_FLUSH_MAX) return hipErrorInvalidValue;
-  const int F = nrb < QF_FLUSH_MAX ? nrb : QF_FLUSH_MAX;
+  const int F = qf_flush_rows(a, NMAT, nrb);
+  if (qf_shape(a.K).P > 1 && F < nrb) return hipErrorInvalidValue;
   if (a.mode == NVFP4) {
     if (a.M == 1) return launch_qf_d<NVFP4, 1, NMAT>(a, w2, s2, grid, F, nrb, st);
     return launch_qf_d<NVFP4, 2, NMAT>(a, w2, s2, grid, F, nrb, st);
@@ -476,8 +674,60 @@ static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8
   }
 }
 
+// nvfp4 on the 32x32x64 form: 32-row blocks, one unit in flight per wave.
+template <int M, int Q, int P>
+static hipError_t launch_q32(const QmmArgs &a, int grid, int F, hipStream_t st) {
+  auto kern = qmv_mfma32_kernel<M, Q, P>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), q32_lds_bytes(M, Q, F), st, (const uint16_t *)a.x, a.w, a.s,
+                     (uint16_t *)a.y, a.N, a.K, F);
+  return hipGetLastError();
+}
+
+static int q32_nrb(const QmmArgs &a, int cus) {
+  const int rbs = (a.N + 15) / 16;
+  const int grid = rbs < cus ? rbs : cus;
+  return ((a.N + grid - 1) / grid + 31) / 32;
+}
+
+static int q32_flush_rows(const QmmArgs &a, int nrb) {
+  int F = nrb < Q32_FLUSH_MAX ? nrb : Q32_FLUSH_MAX;
+  while (F > 1 && q32_lds_bytes(a.M, qf_shape(a.K).Q, F) > QF_LDS_MAX) --F;
+  return F;
+}
+
+static bool q32_ok(const QmmArgs &a) {
+  if (a.mode != NVFP4 || a.x_f32 || a.M < 1 || a.M > 4 || a.N < 16) return false;
+  const QfShape g = qf_shape(a.K);
+  if (g.Q == 0 || qf_cus() == 0) return false;
+  if (g.P > 1 && q32_flush_rows(a, q32_nrb(a, qf_cus())) < q32_nrb(a, qf_cus())) return false;
+  return ((((uintptr_t)a.x) | ((uintptr_t)a.w) | ((uintptr_t)a.s)) & 15) == 0;
+}
+
+static hipError_t launch_q32_any(const QmmArgs &a, hipStream_t st) {
+  if (!q32_ok(a)) return hipErrorInvalidValue;
+  const int cus = qf_cus();
+  const int rbs = (a.N + 15) / 16;
+  const int grid = rbs < cus ? rbs : cus;
+  const int nrb = q32_nrb(a, cus);
+  const int F = q32_flush_rows(a, nrb);
+  const bool three = qf_shape(a.K).P == 3;
+  switch (a.M) {
+    case 1: return three ? launch_q32<1, 12, 3>(a, grid, F, st) : launch_q32<1, 10, 1>(a, grid, F, st);
+    case 2: return three ? launch_q32<2, 12, 3>(a, grid, F, st) : launch_q32<2, 10, 1>(a, grid, F, st);
+    case 3: return three ? launch_q32<3, 12, 3>(a, grid, F, st) : launch_q32<3, 10, 1>(a, grid, F, st);
+    default: return three ? launch_q32<4, 12, 3>(a, grid, F, st) : launch_q32<4, 10, 1>(a, grid, F, st);
+  }
+}
+
 hipError_t launch_qmv_mfma(const QmmArgs &a, hipStream_t st) {
   if (!qmv_mfma_ok(a)) return hipErrorInvalidValue;
+  if (a.mode == NVFP4 && a.M > 2) return launch_q32_any(a, st);
   return launch_qf_any<1>(a, a.w, a.s, st);
 }
 

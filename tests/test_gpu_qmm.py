@@ -350,8 +350,10 @@ def make_x(rng, M, K, kind):
 # Shapes above the MFMA decode path's thresholds (K = 5120: nvfp4 M = 1 from
 # N = 16384, M >= 2 from N = 4096): ragged row blocks (N % 16 != 0), and a row
 # range per workgroup long enough (N = 70001) to need several partial-sum flushes.
+# nvfp4 M = 3-4 runs the 32x32x64 form (32-row blocks, flushes every 4 blocks).
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 1, 70001), ("nvfp4", 2, 4099),
-                                      ("nvfp4", 2, 16384), ("mxfp8", 2, 4101), ("mxfp8", 3, 8192),
+                                      ("nvfp4", 2, 16384), ("nvfp4", 3, 4099), ("nvfp4", 3, 70001),
+                                      ("nvfp4", 4, 16400), ("mxfp8", 2, 4101), ("mxfp8", 3, 8192),
                                       ("mxfp8", 4, 4096), ("mxfp8", 4, 70001)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
 def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
@@ -370,8 +372,9 @@ def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
 # K = 17408 (the MLP down projection): 34 slices of 512 walked by 12 waves in 3
 # passes, the last pass with 2 slices past K.  The edge groups are planted in
 # the first slice of every pass and in the last slice.
-@pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 5120), ("nvfp4", 2, 4099), ("mxfp8", 2, 5120),
-                                      ("mxfp8", 3, 4101), ("mxfp8", 4, 8192)])
+@pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 5120), ("nvfp4", 2, 4099), ("nvfp4", 3, 5120),
+                                      ("nvfp4", 4, 4099), ("mxfp8", 2, 5120), ("mxfp8", 3, 4101),
+                                      ("mxfp8", 4, 8192)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
 def test_decode_mfma_down_shapes_match_oracle(mode, M, N, xkind):
     K = 17408
@@ -389,7 +392,8 @@ def test_decode_mfma_down_shapes_match_oracle(mode, M, N, xkind):
     assert np.array_equal(run_qmm(mode, xb, wq, s), y)
 
 
-@pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 2, 4099), ("mxfp8", 3, 4101)])
+@pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 2, 4099), ("nvfp4", 3, 4099),
+                                      ("mxfp8", 3, 4101)])
 def test_mlp_gate_up_silu_mfma_shapes(mode, M, N):
     """The fused MLP on the MFMA path: equal to two quantized_matmul + silu_mul bit for
     bit, and within tolerance of the oracle's chain on a row sample."""
