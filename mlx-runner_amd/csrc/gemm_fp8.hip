@@ -38,84 +38,100 @@ __host__ __device__ __forceinline__ int64_t packed_scale_index(int64_t r, int b,
   return (((r >> 8) * (K >> 7) + (b >> 2)) * 256 + (r & 255)) * 4 + (b & 3);
 }
 
-// Four lanes per (row, 32-block), eight elements each.  PACKED: scales in the
-// tile-major layout above and hi / lo pre-tiled the way the pipelined GEMM's LDS
-// holds them: for each 256-row tile and 64-wide K step, one contiguous 16 KiB
-// block of 1024 slots of 16 bytes, slot 4 r + (p ^ p_swz(r)) holding bytes
-// [16 p, 16 p + 16) of row r's step.  Otherwise row-major [rows, K] and
-// [rows, K / 32].
+// Two lanes per (row, 32-block), sixteen elements each, so every hi / lo store
+// is one 16-byte slot.  PACKED: scales in the tile-major layout above and hi /
+// lo pre-tiled the way the pipelined GEMM's LDS holds them: for each 256-row
+// tile and 64-wide K step, one contiguous 16 KiB block of 1024 slots of 16
+// bytes, slot 4 r + (p ^ p_swz(r)) holding bytes [16 p, 16 p + 16) of row r's
+// step.  Otherwise row-major [rows, K] and [rows, K / 32].  One thread per
+// (row, half block): rows * K / 16 < 2^31 (checked by the host).
 //
 // hi = RNE_E4M3(x / 2^sh), lo = RNE_E4M3((x - hi * 2^sh) / 2^sl) with the block
 // scales sh, sl from ceil_scale_exp, so no element is clamped.  The rounding is
 // v_cvt_pk_fp8_f32 (OCP E4M3, nearest-even; measured identical to a software
 // nearest-even on every input this pass produces); x - hi * 2^sh is exact in f32.
 template <bool PACKED>
-__global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict__ x, int64_t rows, int K,
+__global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict__ x, uint32_t total, int rows, int K,
                                                       uint8_t *__restrict__ xh, uint8_t *__restrict__ xl,
                                                       uint8_t *__restrict__ sh, uint8_t *__restrict__ sl) {
-  const int nb = K >> 5;
-  const int64_t total = rows * nb * 4;  // a multiple of 4: the four lanes of a block stay together
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int j = (int)(i & 3);
-    const int64_t g = i >> 2, r = g / nb;
-    const int b = (int)(g % nb);
-    const uint4 q = *(const uint4 *)(x + r * K + b * 32 + j * 8);
-    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-    float v[8];
-    float amax = 0.f;
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  // lanes past the end (the grid is whole blocks) compute on a clamped index and
+  // store nothing; total is even, so the two lanes of a block are both live or not
+  const bool live = i < total;
+  const uint32_t ii = live ? i : total - 1;
+  const uint32_t L = (uint32_t)K >> 4;  // threads per row
+  uint32_t r, c;
+  if (PACKED) {
+    // a wave takes 16 rows x one 64-element K step: lane l -> row l / 4, 16
+    // elements l % 4 of the step, so a row's 64 output bytes (one slot row of
+    // the step's block) come from 4 adjacent lanes and the wave writes 1 KiB
+    // of consecutive slots; the reads are 16 whole 128-byte row pieces
+    const uint32_t S = (uint32_t)K >> 6, w = ii >> 6, l = ii & 63;
+    const uint32_t rg = w / S, st = w - rg * S;
+    r = 16 * rg + (l >> 2);
+    c = 4 * st + (l & 3);
+  } else {
+    r = ii / L;
+    c = ii - r * L;
+  }
+  const int b = (int)(c >> 1), j = (int)(c & 1);
+  const uint32_t rl = (int)r < rows ? r : (uint32_t)rows - 1;  // padded rows (packed) read the last row
+  const uint4 *src = (const uint4 *)(x + (int64_t)rl * K + 16 * c);
+  const uint4 q0 = src[0], q1 = src[1];
+  const uint32_t w8[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+  float v[16];
+  float amax = 0.f;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      v[2 * t] = __uint_as_float(w4[t] << 16);
-      v[2 * t + 1] = __uint_as_float(w4[t] & 0xFFFF0000u);
-    }
+  for (int t = 0; t < 8; ++t) {
+    v[2 * t] = __uint_as_float(w8[t] << 16);
+    v[2 * t + 1] = __uint_as_float(w8[t] & 0xFFFF0000u);
+  }
 #pragma unroll
-    for (int t = 0; t < 8; ++t) amax = fmaxf(amax, fabsf(v[t]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    const int th = amax > 0.f ? ceil_scale_exp(amax) : -127;
-    uint32_t hw[2], lw[2];
-    float rmax = 0.f;
+  for (int t = 0; t < 16; ++t) amax = fmaxf(amax, fabsf(v[t]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  const int th = amax > 0.f ? ceil_scale_exp(amax) : -127;
+  uint32_t hw[4], lw[4];
+  float rmax = 0.f;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      int c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t], -th), __builtin_ldexpf(v[4 * t + 1], -th), 0,
-                                              false);
-      c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t + 2], -th), __builtin_ldexpf(v[4 * t + 3], -th), c,
-                                          true);
-      hw[t] = (uint32_t)c;
-      const f32x2_t b0 = __builtin_amdgcn_cvt_pk_f32_fp8(c, false), b1 = __builtin_amdgcn_cvt_pk_f32_fp8(c, true);
-      v[4 * t] -= __builtin_ldexpf(b0.x, th);
-      v[4 * t + 1] -= __builtin_ldexpf(b0.y, th);
-      v[4 * t + 2] -= __builtin_ldexpf(b1.x, th);
-      v[4 * t + 3] -= __builtin_ldexpf(b1.y, th);
+  for (int t = 0; t < 4; ++t) {
+    int cv = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t], -th), __builtin_ldexpf(v[4 * t + 1], -th), 0,
+                                             false);
+    cv = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t + 2], -th), __builtin_ldexpf(v[4 * t + 3], -th), cv,
+                                         true);
+    hw[t] = (uint32_t)cv;
+    const f32x2_t b0 = __builtin_amdgcn_cvt_pk_f32_fp8(cv, false), b1 = __builtin_amdgcn_cvt_pk_f32_fp8(cv, true);
+    v[4 * t] -= __builtin_ldexpf(b0.x, th);
+    v[4 * t + 1] -= __builtin_ldexpf(b0.y, th);
+    v[4 * t + 2] -= __builtin_ldexpf(b1.x, th);
+    v[4 * t + 3] -= __builtin_ldexpf(b1.y, th);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) rmax = fmaxf(rmax, fabsf(v[4 * t + u]));
-    }
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 1));
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 2));
-    const int tl = rmax > 0.f ? ceil_scale_exp(rmax) : -127;
+    for (int u = 0; u < 4; ++u) rmax = fmaxf(rmax, fabsf(v[4 * t + u]));
+  }
+  rmax = fmaxf(rmax, __shfl_xor(rmax, 1));
+  const int tl = rmax > 0.f ? ceil_scale_exp(rmax) : -127;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      int c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t], -tl), __builtin_ldexpf(v[4 * t + 1], -tl), 0,
-                                              false);
-      c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t + 2], -tl), __builtin_ldexpf(v[4 * t + 3], -tl), c,
-                                          true);
-      lw[t] = (uint32_t)c;
-    }
-    int64_t o;  // byte offset of this lane's 8 bytes
-    if (PACKED) {
-      const int64_t blk = ((r >> 8) * (K >> 6) + (b >> 1)) * 16384;
-      const int rr = (int)(r & 255), part = 2 * (b & 1) + (j >> 1);
-      o = blk + 16 * (4 * rr + (part ^ p_swz(rr))) + 8 * (j & 1);
-    } else {
-      o = r * K + b * 32 + 8 * j;
-    }
-    *(uint2 *)(xh + o) = make_uint2(hw[0], hw[1]);
-    *(uint2 *)(xl + o) = make_uint2(lw[0], lw[1]);
-    if (j == 0) {
-      const int64_t so = PACKED ? packed_scale_index(r, b, K) : r * nb + b;
-      sh[so] = (uint8_t)(th + 127);
-      sl[so] = (uint8_t)(tl + 127);
-    }
+  for (int t = 0; t < 4; ++t) {
+    int cv = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t], -tl), __builtin_ldexpf(v[4 * t + 1], -tl), 0,
+                                             false);
+    cv = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t + 2], -tl), __builtin_ldexpf(v[4 * t + 3], -tl), cv,
+                                         true);
+    lw[t] = (uint32_t)cv;
+  }
+  if (!live || (PACKED && r >= rows)) return;
+  int64_t o;  // byte offset of this lane's 16 bytes
+  if (PACKED) {
+    const int64_t blk = ((int64_t)(r >> 8) * (K >> 6) + (b >> 1)) * 16384;
+    const int rr = (int)(r & 255), part = 2 * (b & 1) + j;
+    o = blk + 16 * (4 * rr + (part ^ p_swz(rr)));
+  } else {
+    o = (int64_t)r * K + 16 * c;
+  }
+  *(uint4 *)(xh + o) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  *(uint4 *)(xl + o) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  if (j == 0) {
+    const int64_t so = PACKED ? packed_scale_index(r, b, K) : (int64_t)r * (K >> 5) + b;
+    sh[so] = (uint8_t)(th + 127);
+    sl[so] = (uint8_t)(tl + 127);
   }
 }
 
@@ -489,14 +505,16 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
   uint8_t *xh = (uint8_t *)ws, *xl = xh + mk, *sh = xl + mk, *sl = sh + round256(a.M) * nbk;
   uint8_t *swp = sl + round256(a.M) * nbk;
   const bool pipe = gemm_mxfp8_pipe_ok(a);
-  const int64_t blocks_needed = ((int64_t)a.M * (a.K / 32) * 4 + 255) / 256;
-  const int64_t sb = blocks_needed < 65536 ? blocks_needed : 65536;
+  // one thread per (row, 16 elements); the packed form covers rows in groups of 16
+  const int64_t total = (pipe ? ((int64_t)a.M + 15) / 16 * 16 : (int64_t)a.M) * (a.K / 16);
+  if (total >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+  const unsigned sb = (unsigned)((total + 255) / 256);
   if (pipe)
-    hipLaunchKernelGGL(split_x_kernel<true>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (int64_t)a.M, a.K, xh,
-                       xl, sh, sl);
+    hipLaunchKernelGGL(split_x_kernel<true>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (uint32_t)total, a.M,
+                       a.K, xh, xl, sh, sl);
   else
-    hipLaunchKernelGGL(split_x_kernel<false>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (int64_t)a.M, a.K, xh,
-                       xl, sh, sl);
+    hipLaunchKernelGGL(split_x_kernel<false>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (uint32_t)total,
+                       a.M, a.K, xh, xl, sh, sl);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int tiles = ((a.M + F_BM - 1) / F_BM) * ((a.N + F_BN - 1) / F_BN);
