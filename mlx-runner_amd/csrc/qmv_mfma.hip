@@ -155,15 +155,18 @@ struct QfGeom {
 };
 
 template <int MODE>
-constexpr size_t qf_lds_bytes(int M, int Q, int F, int nmat) {
-  return (size_t)Q * QfGeom<MODE>::WAVE_LDS + (size_t)F * nmat * M * Q * 16 * 4;
+constexpr size_t qf_lds_bytes(int M, int Q, int F) {
+  return (size_t)Q * QfGeom<MODE>::WAVE_LDS + (size_t)F * M * Q * 16 * 4;
 }
 
-// NMAT = 2 is the MLP form (src/model.zig:905-915): W (gate) and W2 (up) are
-// walked row block by row block, unit (rb, 0) then (rb, 1), and the flush
-// writes silu(gate) * up with the reference's bf16 roundings.  The per-row sums
-// are the same as those of two separate NMAT = 1 launches, so fused and
-// unfused results are identical.  D: units whose weights are in flight.
+// NMAT = 2 is the MLP form (src/model.zig:905-915): a unit's 16 MFMA columns
+// are 8 rows of W (gate) and the same 8 rows of W2 (up), so a workgroup walks
+// its output rows in blocks of 8 (as many units as one matrix of twice the
+// rows), and the flush writes silu(gate) * up with the reference's bf16
+// roundings from columns n and n + 8.  Each MFMA column depends on its own
+// weight row only, so the per-row sums are those of two separate NMAT = 1
+// launches and fused and unfused results are identical.  D: units whose
+// weights are in flight.
 //
 // K longer than Q slices is walked in P passes: in pass p wave q owns slice
 // p Q + q (a slice past K re-reads the last slice and its sums are replaced by
@@ -179,16 +182,17 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
   uint8_t *tile = lds + q * G::WAVE_LDS;
-  float *part = (float *)(lds + Q * G::WAVE_LDS);  // [F][NMAT][M][Q][16] partial sums
+  float *part = (float *)(lds + Q * G::WAVE_LDS);  // [F][M][Q][16] partial sums
+  constexpr int RB = NMAT == 2 ? 8 : 16;            // output rows per unit
   const int r_begin = (int)((int64_t)N * blockIdx.x / gridDim.x);
   const int r_end = (int)((int64_t)N * (blockIdx.x + 1) / gridDim.x);
-  const int nrb = (r_end - r_begin + 15) >> 4;
+  const int nrb = (r_end - r_begin + RB - 1) / RB;
   const int S = K >> 9;  // 512-element slices
   auto slice_of = [&](int p) __attribute__((always_inline)) {
     const int sl = p * Q + q;
     return sl < S ? sl : S - 1;
   };
-  const int upp = nrb * NMAT;               // units per pass
+  const int upp = nrb;                      // units per pass
   const int uppd = (upp + D - 1) / D * D;   // ... rounded up to whole buffer groups
 
   // 1) x of this wave's slices, all passes: lane l holds elements [8l, 8l+8) of each row m
@@ -203,22 +207,25 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   constexpr int RPL = MODE == NVFP4 ? 4 : 2;  // rows per load
   constexpr int LPR = 64 / RPL;               // lanes per row
   const int64_t wrow = MODE == NVFP4 ? (K >> 1) : K, srow = MODE == NVFP4 ? (K >> 4) : (K >> 5);
+  // unit row rr of row block rb (NMAT = 2: rr < 8 in W, rr >= 8 the same rows in W2)
   auto row_of = [&](int rb, int rr) __attribute__((always_inline)) {
-    const int row = r_begin + 16 * rb + rr;
+    const int row = r_begin + RB * rb + (NMAT == 2 ? (rr & 7) : rr);
     return row < r_end ? row : r_end - 1;  // rows past the range re-read its last row (results dropped)
   };
-  // unit u = (pass u / uppd, row block (u % uppd) / NMAT, matrix u % NMAT) lives in buffer
-  // u % D; units past a pass's last row block load clamped rows and are not stored
+  // unit u = (pass u / uppd, row block u % uppd) lives in buffer u % D; units past a
+  // pass's last row block load clamped rows and are not stored
   uint4 wv[D][G::LOADS];
   uint32_t sv0[D], sv1[D];
   auto load_unit = [&](int u, int buf) __attribute__((always_inline)) {
-    const int pass = u / uppd, r = u - pass * uppd, rb = r / NMAT, mat = r - rb * NMAT;
+    const int pass = u / uppd, rb = u - pass * uppd;
     const int sl = slice_of(pass < P ? pass : P - 1);
     const int wcol = sl * G::UB + 16 * (lane % LPR), scol = sl * G::SB + (lane & 3) * (G::SB / 4);
-    const uint8_t *wm = mat ? w2 : w, *sm = mat ? s2 : s;
 #pragma unroll
-    for (int i = 0; i < G::LOADS; ++i)
+    for (int i = 0; i < G::LOADS; ++i) {
+      const uint8_t *wm = NMAT == 2 && RPL * i >= 8 ? w2 : w;  // a load's rows are all in one matrix
       wv[buf][i] = load_stream16(wm + row_of(rb, RPL * i + lane / LPR) * wrow + wcol);
+    }
+    const uint8_t *sm = NMAT == 2 && lane >= 32 ? s2 : s;
     const uint8_t *sp = sm + row_of(rb, lane >> 2) * srow + scol;
     if constexpr (MODE == NVFP4) {
       const uint2 t2 = *(const uint2 *)sp;
@@ -277,17 +284,17 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   // sum the waves' partials of row blocks [rb_first, rb_last] in wave order
   auto flush = [&](int rb_first, int rb_last) __attribute__((always_inline)) {
     lds_barrier();
-    const int items = (rb_last - rb_first + 1) * M * 16;
+    const int items = (rb_last - rb_first + 1) * M * RB;
     for (int t = tid; t < items; t += 64 * Q) {
-      const int nn = t & 15, m = (t >> 4) % M, rbi = (t >> 4) / M;
-      const int rb = rb_first + rbi, row = r_begin + 16 * rb + nn;
+      const int nn = t % RB, m = (t / RB) % M, rbi = t / (RB * M);
+      const int rb = rb_first + rbi, row = r_begin + RB * rb + nn;
+      const float *pp = part + (((rb % F) * M + m) * Q) * 16 + nn;
       float sum[NMAT];
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat) {
-        const float *pp = part + ((((rb % F) * NMAT + mat) * M + m) * Q) * 16 + nn;
         sum[mat] = 0.f;
 #pragma unroll
-        for (int qq = 0; qq < Q; ++qq) sum[mat] += pp[16 * qq];
+        for (int qq = 0; qq < Q; ++qq) sum[mat] += pp[16 * qq + 8 * mat];
       }
       const float out = NMAT == 2 ? silu_mul_bf16(sum[0], sum[NMAT - 1]) : sum[0];
       if (row < r_end) y[(int64_t)m * N + row] = f32_to_bf16_rne(out);
@@ -305,7 +312,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
    for (int r0 = 0; r0 < uppd; r0 += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      const int r = r0 + d, rb = r / NMAT, mat = r - rb * NMAT;
+      const int r = r0 + d, rb = r;
       // unit u: registers -> tile (the x records are no longer needed there), then refill
       // the buffer with unit u + D (past the last unit: clamped rows, unused)
 #pragma unroll
@@ -320,7 +327,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
       // a slice past K (last pass only) re-read the last slice: its sums are dropped
       const bool real = P == 1 || p * Q + q < S;
       const int rbf = rb % F;
-      float *pslot = part + ((rbf * NMAT + mat) * M) * Q * 16;
+      float *pslot = part + (rbf * M) * Q * 16;
       if constexpr (MODE == NVFP4) {
         float acc[M];
 #pragma unroll
@@ -379,7 +386,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
         for (int c = 0; c < 4; ++c) keep_live(bsc[c]);
       }
       // with several passes the host sets F >= nrb: one flush, after the last pass
-      if (live && p == P - 1 && mat == NMAT - 1 && ((rb + 1) % F == 0 || rb + 1 == nrb)) flush(rb - rbf, rb);
+      if (live && p == P - 1 && ((rb + 1) % F == 0 || rb + 1 == nrb)) flush(rb - rbf, rb);
     }
    }
   }
@@ -574,20 +581,21 @@ static int qf_cus() {
   return cus;
 }
 
-static int qf_nrb(const QmmArgs &a, int cus) {
+// Units per workgroup: row blocks of 16 rows (8 output rows in the MLP form).
+static int qf_nrb(const QmmArgs &a, int cus, int nmat = 1) {
   const int rbs = (a.N + 15) / 16;
   const int grid = rbs < cus ? rbs : cus;
-  return ((a.N + grid - 1) / grid + 15) / 16;
+  const int rb = nmat == 2 ? 8 : 16;
+  return ((a.N + grid - 1) / grid + rb - 1) / rb;
 }
 
 constexpr size_t QF_LDS_MAX = 160 * 1024;
 
 // Row blocks per partial-sum flush: up to QF_FLUSH_MAX, as many as fit the LDS.
-static int qf_flush_rows(const QmmArgs &a, int nmat, int nrb) {
+static int qf_flush_rows(const QmmArgs &a, int nrb) {
   const QfShape g = qf_shape(a.K);
   int F = nrb < QF_FLUSH_MAX ? nrb : QF_FLUSH_MAX;
-  while (F > 1 && (a.mode == NVFP4 ? qf_lds_bytes<NVFP4>(a.M, g.Q, F, nmat) : qf_lds_bytes<MXFP8>(a.M, g.Q, F, nmat)) >
-                      QF_LDS_MAX)
+  while (F > 1 && (a.mode == NVFP4 ? qf_lds_bytes<NVFP4>(a.M, g.Q, F) : qf_lds_bytes<MXFP8>(a.M, g.Q, F)) > QF_LDS_MAX)
     --F;
   return F;
 }
@@ -612,7 +620,7 @@ bool qmv_mfma_ok(const QmmArgs &a) {
   if (a.M == 1 && (a.mode != NVFP4 || (g.P == 1 && a.N < 16384))) return false;
   if (a.N < 4096) return false;
   // several passes keep every row block's partial sums in LDS
-  if (g.P > 1 && (qf_cus() == 0 || qf_flush_rows(a, 1, qf_nrb(a, qf_cus())) < qf_nrb(a, qf_cus()))) return false;
+  if (g.P > 1 && (qf_cus() == 0 || qf_flush_rows(a, qf_nrb(a, qf_cus())) < qf_nrb(a, qf_cus()))) return false;
   if ((((uintptr_t)a.x) | ((uintptr_t)a.w)) & 15) return false;
   if (((uintptr_t)a.s) & 7) return false;  // scale slices are read as 8 (nvfp4) / 4 (mxfp8) bytes
   return true;
@@ -628,7 +636,7 @@ template <int MODE, int M, int Q, int NMAT, int D, int P>
 static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
                             hipStream_t st) {
   auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D, P>;
-  const size_t lds = qf_lds_bytes<MODE>(M, Q, F, NMAT);
+  const size_t lds = qf_lds_bytes<MODE>(M, Q, F);
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -649,7 +657,9 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
                               hipStream_t st) {
   if constexpr (NMAT == 1)
     if (qf_shape(a.K).P == 3) return launch_qf<MODE, M, 12, 1, 1, 3>(a, w2, s2, grid, F, st);
-  if (nrb * NMAT <= 4) return launch_qf<MODE, M, 10, NMAT, 2, 1>(a, w2, s2, grid, F, st);
+  // (the MLP form at nvfp4 M = 2 would spill with two units in flight)
+  if constexpr (!(NMAT == 2 && MODE == NVFP4 && M == 2))
+    if (nrb <= 4) return launch_qf<MODE, M, 10, NMAT, 2, 1>(a, w2, s2, grid, F, st);
   return launch_qf<MODE, M, 10, NMAT, 1, 1>(a, w2, s2, grid, F, st);
 }
 
@@ -659,8 +669,8 @@ static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8
   if (cus == 0) return hipErrorNoDevice;
   const int rbs = (a.N + 15) / 16;
   const int grid = rbs < cus ? rbs : cus;
-  const int nrb = qf_nrb(a, cus);
-  const int F = qf_flush_rows(a, NMAT, nrb);
+  const int nrb = qf_nrb(a, cus, NMAT);
+  const int F = qf_flush_rows(a, nrb);
   if (qf_shape(a.K).P > 1 && F < nrb) return hipErrorInvalidValue;
   if (a.mode == NVFP4) {
     if (a.M == 1) return launch_qf_d<NVFP4, 1, NMAT>(a, w2, s2, grid, F, nrb, st);
