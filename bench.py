@@ -54,6 +54,11 @@ CONFIGS = {
     "mlp_gateup_silu": dict(mode="nvfp4", M=1, N=17408, K=5120, xscale=1.0, mlp=True,
                             workload="nvfp4 MLP gate+up+SiLU*mul fused decode GEMV, x bf16 [1,5120], "
                                      "W_gate, W_up [17408,5120]"),
+    "mlp_gateup_silu_m3": dict(mode="nvfp4", M=3, N=17408, K=5120, xscale=1.0, mlp=True,
+                               workload="nvfp4 MLP gate+up+SiLU*mul fused MTP-verify skinny GEMM, x bf16 [3,5120], "
+                                        "W_gate, W_up [17408,5120]"),
+    "gateup_m3": dict(mode="nvfp4", M=3, N=34816, K=5120, xscale=1.0,
+                      workload="nvfp4 gate+up MTP-verify skinny GEMM, x bf16 [3,5120], W [34816,5120]"),
     "dense_lmhead": dict(mode="bf16", M=1, N=248320, K=5120, xscale=1.0,
                          workload="dense bf16 lm_head decode GEMV (mxfp8 checkpoints), x bf16 [1,5120], "
                                   "W bf16 [248320,5120]"),

@@ -416,18 +416,23 @@ constexpr int Q32_WAVE_LDS = Q32_TILE > 4 * 4 * QF_REC + 4 * 64 ? Q32_TILE : 4 *
 constexpr int Q32_FLUSH_MAX = 4;
 constexpr size_t q32_lds_bytes(int M, int Q, int F) { return (size_t)Q * Q32_WAVE_LDS + (size_t)F * M * Q * 64 * 4; }
 
-template <int M, int Q, int P>
+// NMAT = 2: the MLP form, a unit's 32 columns being 16 rows of W (gate) and the
+// same 16 rows of W2 (up); the flush writes silu(gate) * up (as in qmv_mfma_kernel).
+template <int M, int Q, int P, int NMAT>
 __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__restrict__ x,
                                                             const uint8_t *__restrict__ w,
-                                                            const uint8_t *__restrict__ s, uint16_t *__restrict__ y,
+                                                            const uint8_t *__restrict__ s,
+                                                            const uint8_t *__restrict__ w2,
+                                                            const uint8_t *__restrict__ s2, uint16_t *__restrict__ y,
                                                             int N, int K, int F) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
   uint8_t *tile = lds + q * Q32_WAVE_LDS;
   float *part = (float *)(lds + Q * Q32_WAVE_LDS);  // [F][M][Q][2][32] partial sums (wave, lane half)
+  constexpr int RB = NMAT == 2 ? 16 : 32;            // output rows per unit
   const int r_begin = (int)((int64_t)N * blockIdx.x / gridDim.x);
   const int r_end = (int)((int64_t)N * (blockIdx.x + 1) / gridDim.x);
-  const int nrb = (r_end - r_begin + 31) >> 5;
+  const int nrb = (r_end - r_begin + RB - 1) / RB;
   const int S = K >> 9;
   auto slice_of = [&](int p) __attribute__((always_inline)) {
     const int sl = p * Q + q;
@@ -444,8 +449,9 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
   // unit u = (pass u / nrb, row block u % nrb).  Load i, lane l: row 4i + l/16,
   // bytes 16 (l%16) of the slice; scales: lane l, row l/2, bytes 16 (l%2).
   const int64_t wrow = K >> 1, srow = K >> 4;
+  // unit row rr of row block rb (NMAT = 2: rr < 16 in W, rr >= 16 the same rows in W2)
   auto row_of = [&](int rb, int rr) __attribute__((always_inline)) {
-    const int row = r_begin + 32 * rb + rr;
+    const int row = r_begin + RB * rb + (NMAT == 2 ? (rr & 15) : rr);
     return row < r_end ? row : r_end - 1;  // rows past the range re-read its last row (results dropped)
   };
   uint4 wv[8], sv;
@@ -453,9 +459,12 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
     const int pass = u / nrb, rb = u - pass * nrb;
     const int sl = slice_of(pass < P ? pass : P - 1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      wv[i] = load_stream16(w + row_of(rb, 4 * i + (lane >> 4)) * wrow + sl * 256 + 16 * (lane & 15));
-    sv = *(const uint4 *)(s + row_of(rb, lane >> 1) * srow + sl * 32 + 16 * (lane & 1));
+    for (int i = 0; i < 8; ++i) {
+      const uint8_t *wm = NMAT == 2 && i >= 4 ? w2 : w;  // a load's rows are all in one matrix
+      wv[i] = load_stream16(wm + row_of(rb, 4 * i + (lane >> 4)) * wrow + sl * 256 + 16 * (lane & 15));
+    }
+    const uint8_t *sm = NMAT == 2 && lane >= 32 ? s2 : s;
+    sv = *(const uint4 *)(sm + row_of(rb, lane >> 1) * srow + sl * 32 + 16 * (lane & 1));
   };
   load_unit(0);
 
@@ -483,15 +492,20 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
 
   auto flush = [&](int rb_first, int rb_last) __attribute__((always_inline)) {
     lds_barrier();
-    const int items = (rb_last - rb_first + 1) * M * 32;
+    const int items = (rb_last - rb_first + 1) * M * RB;
     for (int t = tid; t < items; t += 64 * Q) {
-      const int nn = t & 31, m = (t >> 5) % M, rbi = (t >> 5) / M;
-      const int rb = rb_first + rbi, row = r_begin + 32 * rb + nn;
+      const int nn = t % RB, m = (t / RB) % M, rbi = t / (RB * M);
+      const int rb = rb_first + rbi, row = r_begin + RB * rb + nn;
       const float *pp = part + (((rb % F) * M + m) * Q) * 64 + nn;
-      float sum = 0.f;
+      float sum[NMAT];
 #pragma unroll
-      for (int qh = 0; qh < 2 * Q; ++qh) sum += pp[32 * qh];
-      if (row < r_end) y[(int64_t)m * N + row] = f32_to_bf16_rne(sum);
+      for (int mat = 0; mat < NMAT; ++mat) {
+        sum[mat] = 0.f;
+#pragma unroll
+        for (int qh = 0; qh < 2 * Q; ++qh) sum[mat] += pp[32 * qh + 16 * mat];
+      }
+      const float out = NMAT == 2 ? silu_mul_bf16(sum[0], sum[NMAT - 1]) : sum[0];
+      if (row < r_end) y[(int64_t)m * N + row] = f32_to_bf16_rne(out);
     }
     lds_barrier();
   };
@@ -626,10 +640,14 @@ bool qmv_mfma_ok(const QmmArgs &a) {
   return true;
 }
 
-// The fused MLP form exists for the 16x16x128 kernel only (nvfp4 M <= 2, mxfp8 M <= 4).
+static bool q32_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up);
+
+// The fused MLP form: the 16x16x128 kernel (nvfp4 M <= 2, mxfp8 M <= 4) and the
+// 32x32x64 kernel at one pass (nvfp4 M = 3-4, K = 5120).
 bool qmv_mfma_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up) {
-  if (a.mode == NVFP4 && a.M > 2) return false;
-  return qmv_mfma_ok(a) && (((uintptr_t)w_up) & 15) == 0 && (((uintptr_t)s_up) & 7) == 0;
+  if (!qmv_mfma_ok(a)) return false;
+  if (a.mode == NVFP4 && a.M > 2) return q32_mlp_ok(a, w_up, s_up);
+  return (((uintptr_t)w_up) & 15) == 0 && (((uintptr_t)s_up) & 7) == 0;
 }
 
 template <int MODE, int M, int Q, int NMAT, int D, int P>
@@ -685,24 +703,27 @@ static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8
 }
 
 // nvfp4 on the 32x32x64 form: 32-row blocks, one unit in flight per wave.
-template <int M, int Q, int P>
-static hipError_t launch_q32(const QmmArgs &a, int grid, int F, hipStream_t st) {
-  auto kern = qmv_mfma32_kernel<M, Q, P>;
+template <int M, int Q, int P, int NMAT>
+static hipError_t launch_q32(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
+                             hipStream_t st) {
+  auto kern = qmv_mfma32_kernel<M, Q, P, NMAT>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), q32_lds_bytes(M, Q, F), st, (const uint16_t *)a.x, a.w, a.s,
-                     (uint16_t *)a.y, a.N, a.K, F);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), q32_lds_bytes(M, Q, F), st, (const uint16_t *)a.x, a.w, a.s, w2,
+                     s2, (uint16_t *)a.y, a.N, a.K, F);
   return hipGetLastError();
 }
 
-static int q32_nrb(const QmmArgs &a, int cus) {
+// Units per workgroup: row blocks of 32 rows (16 output rows in the MLP form).
+static int q32_nrb(const QmmArgs &a, int cus, int nmat = 1) {
   const int rbs = (a.N + 15) / 16;
   const int grid = rbs < cus ? rbs : cus;
-  return ((a.N + grid - 1) / grid + 31) / 32;
+  const int rb = nmat == 2 ? 16 : 32;
+  return ((a.N + grid - 1) / grid + rb - 1) / rb;
 }
 
 static int q32_flush_rows(const QmmArgs &a, int nrb) {
@@ -727,12 +748,29 @@ static hipError_t launch_q32_any(const QmmArgs &a, hipStream_t st) {
   const int nrb = q32_nrb(a, cus);
   const int F = q32_flush_rows(a, nrb);
   const bool three = qf_shape(a.K).P == 3;
+  const uint8_t *w2 = a.w, *s2 = a.s;  // unused in the plain form
   switch (a.M) {
-    case 1: return three ? launch_q32<1, 12, 3>(a, grid, F, st) : launch_q32<1, 10, 1>(a, grid, F, st);
-    case 2: return three ? launch_q32<2, 12, 3>(a, grid, F, st) : launch_q32<2, 10, 1>(a, grid, F, st);
-    case 3: return three ? launch_q32<3, 12, 3>(a, grid, F, st) : launch_q32<3, 10, 1>(a, grid, F, st);
-    default: return three ? launch_q32<4, 12, 3>(a, grid, F, st) : launch_q32<4, 10, 1>(a, grid, F, st);
+    case 1: return three ? launch_q32<1, 12, 3, 1>(a, w2, s2, grid, F, st) : launch_q32<1, 10, 1, 1>(a, w2, s2, grid, F, st);
+    case 2: return three ? launch_q32<2, 12, 3, 1>(a, w2, s2, grid, F, st) : launch_q32<2, 10, 1, 1>(a, w2, s2, grid, F, st);
+    case 3: return three ? launch_q32<3, 12, 3, 1>(a, w2, s2, grid, F, st) : launch_q32<3, 10, 1, 1>(a, w2, s2, grid, F, st);
+    default: return three ? launch_q32<4, 12, 3, 1>(a, w2, s2, grid, F, st) : launch_q32<4, 10, 1, 1>(a, w2, s2, grid, F, st);
   }
+}
+
+// The MLP form at nvfp4 M = 3-4 (K = 5120, one pass).
+static bool q32_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up) {
+  return a.M >= 3 && q32_ok(a) && qf_shape(a.K).P == 1 && ((((uintptr_t)w_up) | ((uintptr_t)s_up)) & 15) == 0;
+}
+
+static hipError_t launch_q32_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st) {
+  if (!q32_mlp_ok(a, w_up, s_up)) return hipErrorInvalidValue;
+  const int cus = qf_cus();
+  const int rbs = (a.N + 15) / 16;
+  const int grid = rbs < cus ? rbs : cus;
+  const int nrb = q32_nrb(a, cus, 2);
+  const int F = q32_flush_rows(a, nrb);
+  if (a.M == 3) return launch_q32<3, 10, 1, 2>(a, w_up, s_up, grid, F, st);
+  return launch_q32<4, 10, 1, 2>(a, w_up, s_up, grid, F, st);
 }
 
 hipError_t launch_qmv_mfma(const QmmArgs &a, hipStream_t st) {
@@ -743,6 +781,7 @@ hipError_t launch_qmv_mfma(const QmmArgs &a, hipStream_t st) {
 
 hipError_t launch_qmv_mfma_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st) {
   if (!qmv_mfma_mlp_ok(a, w_up, s_up)) return hipErrorInvalidValue;
+  if (a.mode == NVFP4 && a.M > 2) return launch_q32_mlp(a, w_up, s_up, st);
   return launch_qf_any<2>(a, w_up, s_up, st);
 }
 

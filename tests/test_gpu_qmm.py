@@ -393,7 +393,7 @@ def test_decode_mfma_down_shapes_match_oracle(mode, M, N, xkind):
 
 
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 2, 4099), ("nvfp4", 3, 4099),
-                                      ("mxfp8", 3, 4101)])
+                                      ("nvfp4", 4, 16400), ("mxfp8", 3, 4101), ("mxfp8", 4, 70001)])
 def test_mlp_gate_up_silu_mfma_shapes(mode, M, N):
     """The fused MLP on the MFMA path: equal to two quantized_matmul + silu_mul bit for
     bit, and within tolerance of the oracle's chain on a row sample."""
