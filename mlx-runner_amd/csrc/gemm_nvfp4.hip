@@ -9,19 +9,22 @@
 //
 // Same pipeline as the mxfp8 kernel: 256 x 256 block tile, K step 64, 8 waves
 // in two ping-pong groups, a 3-stage LDS ring filled by LDS DMA two steps ahead,
-// one barrier per interval.  Per stage:
+// one barrier per interval.  The 64 elements of a step are taken in an order
+// of our choosing (the same for x and W, so the sum is unchanged): K sub-step
+// ks (of 4) takes elements 8 ks + [0, 8) for operand lane half 0 and
+// 32 + 8 ks + [0, 8) for half 1, so a lane's four 8-element W pieces are one
+// contiguous 16-byte piece of its row.  Per stage:
 //   * x tile, 256 rows x 64 bf16 (128 bytes per row, moved in whole 128-byte
 //     row segments); 16-byte slot S of row r stored at slot S ^ aswz(r);
-//   * W tile kept in nvfp4, 256 rows x 32 bytes, moved by dword DMA and permuted
-//     so that a lane's four 8-element pieces (one per 16-wide K sub-step, the
-//     lane's half of it) are one 16-byte LDS read: dword (h, ks) of a row holds
-//     global dword 2 ks + h, the two 16-byte halves swapped by wswz(r);
+//   * W tile kept in nvfp4, 256 rows x 32 bytes, row-major, moved by one
+//     16-byte-per-lane DMA per wave (32 rows);
 //   * the step's E4M3 scales, one dword (4 groups of 16) per W row, from the
 //     tile-major repacked copy.
 // Each wave owns 128 x 64 of the tile (4 x 2 accumulators).  The loading
-// interval reads the wave's W fragments and scales; the computing interval reads
-// x fragments per K sub-step and dequantizes W in registers (E2M1 -> f32, times
-// the scale, -> bf16: exact), interleaved with the MFMAs.
+// interval reads the wave's W fragments and scales and dequantizes them in
+// registers (E2M1 -> f32, times the scale, -> bf16: exact), beside the other
+// group's MFMAs; the computing interval reads x fragments per K sub-step and
+// runs the MFMAs.
 #include <type_traits>
 
 #include "gemm_pipe.h"
@@ -34,15 +37,15 @@ namespace {
 constexpr int V_BM = 256, V_BN = 256, V_BK = 64, V_THREADS = 512;
 constexpr int V_ATILE = 256 * 128;                 // x: 256 rows x 64 bf16
 constexpr int V_WTILE = 256 * 32;                  // W: 256 rows x 64 nvfp4
-constexpr int V_STILE = 2 * 1024;                  // scale dwords + 1 KiB spare
-constexpr int V_STAGE = V_ATILE + V_WTILE + V_STILE;  // 42 KiB
+constexpr int V_STILE = 1024;                      // scale dwords
+constexpr int V_STAGE = V_ATILE + V_WTILE + V_STILE;  // 41 KiB
 constexpr int V_STAGES = 3;
-constexpr size_t V_LDS = (size_t)V_STAGES * V_STAGE;  // 126 KiB
-constexpr int V_DMA = 9;                              // DMAs per wave per step: 4 x, 4 W, 1 scale
+constexpr size_t V_LDS = (size_t)V_STAGES * V_STAGE;  // 123 KiB
+// DMAs per wave per step: 4 x, 1 W, and for wave 0 the step's 256 scale dwords (1 KiB, one DMA)
+constexpr int V_DMA_S = 6, V_DMA = 5;
 }  // namespace
 
 __device__ __forceinline__ int aswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-__device__ __forceinline__ int wswz(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
 
 // 8 nvfp4 elements (one dword, lowest nibble first) times the E4M3 scale byte, as 8 bf16.
 __device__ __forceinline__ bf16x8_t deq8_nvfp4(uint32_t word, uint32_t scale_byte) {
@@ -79,41 +82,41 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
   const int64_t wrow = K >> 1;  // bytes per W row
 
   // DMA sources (step 0).  x: wave-instruction g = wave + 8 i fills slots q = 64 g + lane.
-  const uint8_t *ga[4], *gw[4];
+  const uint8_t *ga[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int g = wave + 8 * i;
     const int q = 64 * g + lane, row = q >> 3, part = (q & 7) ^ aswz(row);
     ga[i] = (const uint8_t *)x + ((int64_t)min(m0 + row, M - 1) * K + part * 8) * 2;
-    // W: dword slot d = 64 g + lane of the tile: row d >> 3, physical half hp, sub-step ks
-    const int d = 64 * g + lane, wr = d >> 3, hp = (d >> 2) & 1, ks = d & 3, h = hp ^ wswz(wr);
-    gw[i] = w + (int64_t)min(n0 + wr, N - 1) * wrow + 4 * (2 * ks + h);
   }
-  // scales: wave-instruction t = wave copies rows (t % 4) * 64 + lane of the step's 1 KiB block
-  // (t >= 4 re-read the same rows into the spare KiB)
-  const uint8_t *gs = sp + ((int64_t)tn * steps * 256 + (wave & 3) * 64 + lane) * 4;
+  // W: wave w moves rows 32 w + lane / 2, bytes 16 (lane % 2) of the step's 32
+  const uint8_t *gw = w + (int64_t)min(n0 + 32 * wave + (lane >> 1), N - 1) * wrow + 16 * (lane & 1);
+  // scales: wave 0, lane l copies the scale dwords of rows 4 l .. 4 l + 3 (the step's 1 KiB block)
+  const uint8_t *gs = sp + ((int64_t)tn * steps * 256 + 4 * lane) * 4;
+  const bool sw = wave == 0;
   auto issue = [&](int s) __attribute__((always_inline)) {
     const uint32_t st = lds0 + (uint32_t)((s % V_STAGES) * V_STAGE);
 #pragma unroll
     for (int i = 0; i < 4; ++i) gp_dma16(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) gp_dma4(gw[i] + s * 32, st + V_ATILE + (wave + 8 * i) * 256);
-    gp_dma4(gs + s * 1024, st + V_ATILE + V_WTILE + wave * 256);
+    gp_dma16(gw + s * 32, st + V_ATILE + wave * 1024);
+    if (sw) gp_dma16(gs + s * 1024, st + V_ATILE + V_WTILE);
   };
 
-  // fragment geometry (32x32x16 bf16 operands: lane l holds row l % 32, K 8 (l / 32) + [0, 8) of the sub-step)
+  // fragment geometry (32x32x16 bf16 operands: lane l holds row l % 32 and, in
+  // sub-step ks, the step's elements 32 fh + 8 ks + [0, 8) with fh = l / 32:
+  // x slot 4 fh + ks, W dword 4 fh + ks)
   const int fr = lane & 31, fh = lane >> 5;
   int oa[4], ab[4], ob[2], os[2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = wm * 128 + i * 32 + fr;
     oa[i] = r * 128;
-    ab[i] = fh ^ aswz(r);  // physical slot of logical slot 2 ks + fh is 2 ks ^ ab
+    ab[i] = (4 * fh) ^ aswz(r);  // physical slot of logical slot 4 fh + ks is ks ^ ab
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int r = wn * 64 + j * 32 + fr;
-    ob[j] = V_ATILE + r * 32 + 16 * (fh ^ wswz(r));
+    ob[j] = V_ATILE + r * 32 + 16 * fh;
     os[j] = V_ATILE + V_WTILE + r * 4;
   }
 
@@ -132,12 +135,13 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
   // which refills stage k - 1, is issued by both groups in interval 2k + 1
   // (group 0 at the start of its computing interval, group 1 in its loading
   // interval); at the barrier ending interval 2k + 1 every wave waits for its
-  // DMA(k + 1) (only DMA(k + 2), V_DMA loads, may remain in flight).
+  // DMA(k + 1) (only DMA(k + 2), V_DMA_S / V_DMA loads, may remain in flight).
   const int grp = wave >> 2;
   issue(0);
   if (steps > 1) issue(1);
-  if (steps > 1) gp_wait_barrier<V_DMA>();
-  else gp_wait_barrier<0>();
+  if (steps <= 1) gp_wait_barrier<0>();
+  else if (sw) gp_wait_barrier<V_DMA_S>();
+  else gp_wait_barrier<V_DMA>();
 
   auto pp_step = [&](auto grp_c, auto dma_c, int s) __attribute__((always_inline)) {
     constexpr int GRP = decltype(grp_c)::value;
@@ -151,33 +155,56 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
       wq[j] = *(const uint4 *)(st + ob[j]);
       wsc[j] = *(const uint32_t *)(st + os[j]);
     }
+    // W is dequantized here, in the loading interval, so that this VALU work runs
+    // beside the other group's MFMAs and the computing interval is MFMAs only
+    bf16x8_t bf[4][2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t word = ks == 0 ? wq[j].x : ks == 1 ? wq[j].y : ks == 2 ? wq[j].z : wq[j].w;
+        bf[ks][j] = deq8_nvfp4(word, (wsc[j] >> (8 * (2 * fh + (ks >> 1)))) & 0xFF);  // group 2 fh + ks / 2
+      }
+    // the first sub-step's x fragments too (the stage is complete since the last barrier)
+    bf16x8_t af[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[0][i] = *(const bf16x8_t *)(st + oa[i] + 16 * ab[i]);  // ks = 0
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (GRP == 0) gp_lds_barrier();
     else if constexpr (DMA) gp_wait_barrier<V_DMA>();
     else gp_wait_barrier<0>();
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (DMA && GRP == 0) issue(s + 2);  // interval 2s + 1
-    // computing interval: x fragments are read per K sub-step, W fragments
-    // dequantized in place
+    // computing interval: sub-step ks + 1's x fragments are read while sub-step
+    // ks's eight MFMAs run
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      bf16x8_t af[4], bf[2];
+      if (ks < 3) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = *(const bf16x8_t *)(st + oa[i] + 16 * ((2 * ks) ^ ab[i]));
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const uint32_t word = ks == 0 ? wq[j].x : ks == 1 ? wq[j].y : ks == 2 ? wq[j].z : wq[j].w;
-        bf[j] = deq8_nvfp4(word, (wsc[j] >> (8 * ks)) & 0xFF);
+        for (int i = 0; i < 4; ++i)
+          af[(ks + 1) & 1][i] = *(const bf16x8_t *)(st + oa[i] + 16 * ((ks + 1) ^ ab[i]));
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < 4; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bf[ks][j], acc[i][j], 0, 0, 0);
     }
+    // keep that order: the scheduler would otherwise sink each read next to its use
+#pragma unroll
+    for (int ks = 0; ks < 3; ++ks) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // 4 LDS reads (sub-step ks + 1)
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // then sub-step ks's 8 MFMAs
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (GRP == 1) gp_lds_barrier();
-    else if constexpr (DMA) gp_wait_barrier<V_DMA>();
-    else gp_wait_barrier<0>();
+    else if constexpr (DMA) {
+      if (sw) gp_wait_barrier<V_DMA_S>();
+      else gp_wait_barrier<V_DMA>();
+    } else {
+      gp_wait_barrier<0>();
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
   auto pp_run = [&](auto grp_c) __attribute__((always_inline)) {
@@ -207,11 +234,11 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
 
 static size_t round256v(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// K % 64 (whole steps; the scale dword of a step is 4 groups); x rows 16-byte and
-// W rows / scale rows 4-byte aligned for the DMA and the repack.
+// K % 64 (whole steps; the scale dword of a step is 4 groups); x and W rows
+// 16-byte aligned for the DMA, scale rows 4-byte aligned for the repack.
 bool gemm_nvfp4_ok(const QmmArgs &a) {
   return a.mode == NVFP4 && !a.x_f32 && a.K % V_BK == 0 && a.K > 0 && a.M > 0 && a.N > 0 &&
-         (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.w % 4 == 0 && (uintptr_t)a.s % 4 == 0;
+         (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.w % 16 == 0 && (uintptr_t)a.s % 4 == 0;
 }
 
 size_t gemm_nvfp4_workspace(const QmmArgs &a) { return round256v(a.N) * (size_t)(a.K / 16) + 256; }
