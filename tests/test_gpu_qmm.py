@@ -241,6 +241,23 @@ def test_prefill_matches_oracle(mode, M, N, K):
     assert ok, (fro, worst)
 
 
+# The pipelined prefill GEMMs on weights over every code (all E2M1 nibbles / every
+# finite E4M3 byte) and x with the edge groups: ragged N and M, several K steps,
+# and the down projection's K = 17408 (checked on a column sample).
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+@pytest.mark.parametrize("M,N,K", [(257, 1000, 1024), (40, 4099, 5120), (520, 384, 17408)])
+def test_prefill_pipe_edge_values(mode, M, N, K):
+    rng = np.random.default_rng(3 * M + N + K)
+    wq, s = rand_packed(rng, mode, N, K)
+    xb = make_x(rng, M, K, "edge")
+    y = run_qmm(mode, xb, wq, s)
+    cols = np.unique(np.concatenate([np.arange(0, N, max(1, N // 97)), np.arange(N - 9, N)]))
+    ref = O.qmm(mode, xb, wq, s, cols=cols)
+    ok, fro, worst = O.check_tolerance(f32(y[:, cols]), f32(ref), **TOL)
+    assert ok, (fro, worst)
+    assert np.array_equal(run_qmm(mode, xb, wq, s), y)
+
+
 def test_rank3_x_and_inplace_output():
     """x [1, T, K] (the model's layer input, src/model.zig:1284) -> y [1, T, N]; a preallocated
     output of the exact shape is written in place."""
