@@ -216,17 +216,30 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   // pass's last row block load clamped rows and are not stored
   uint4 wv[D][G::LOADS];
   uint32_t sv0[D], sv1[D];
-  auto load_unit = [&](int u, int buf) __attribute__((always_inline)) {
-    const int pass = u / uppd, rb = u - pass * uppd;
+  // W addresses are 32-bit offsets from the matrix base (the host checks that a
+  // matrix is under 4 GiB; fewer registers, and the loads take the base from
+  // scalar registers), the scales' from this lane's base.
+  struct UnitAddr {
+    uint32_t wo[G::LOADS], so;  // byte offsets in W (or W2) and in the scales
+  };
+  const uint8_t *sbase = NMAT == 2 && lane >= 32 ? s2 : s;  // this lane's scale rows
+  auto wbase = [&](int i) __attribute__((always_inline)) {
+    return NMAT == 2 && RPL * i >= 8 ? w2 : w;  // a load's rows are all in one matrix
+  };
+  auto unit_addr = [&](int u) __attribute__((always_inline)) {
+    const int pass = P == 1 ? 0 : u / uppd, rb = u - pass * uppd;
     const int sl = slice_of(pass < P ? pass : P - 1);
     const int wcol = sl * G::UB + 16 * (lane % LPR), scol = sl * G::SB + (lane & 3) * (G::SB / 4);
+    UnitAddr a;
 #pragma unroll
-    for (int i = 0; i < G::LOADS; ++i) {
-      const uint8_t *wm = NMAT == 2 && RPL * i >= 8 ? w2 : w;  // a load's rows are all in one matrix
-      wv[buf][i] = load_stream16(wm + row_of(rb, RPL * i + lane / LPR) * wrow + wcol);
-    }
-    const uint8_t *sm = NMAT == 2 && lane >= 32 ? s2 : s;
-    const uint8_t *sp = sm + row_of(rb, lane >> 2) * srow + scol;
+    for (int i = 0; i < G::LOADS; ++i) a.wo[i] = (uint32_t)row_of(rb, RPL * i + lane / LPR) * (uint32_t)wrow + wcol;
+    a.so = (uint32_t)row_of(rb, lane >> 2) * (uint32_t)srow + scol;
+    return a;
+  };
+  auto load_from = [&](const UnitAddr &a, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < G::LOADS; ++i) wv[buf][i] = load_stream16(wbase(i) + a.wo[i]);
+    const uint8_t *sp = sbase + a.so;
     if constexpr (MODE == NVFP4) {
       const uint2 t2 = *(const uint2 *)sp;
       sv0[buf] = t2.x;
@@ -236,7 +249,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
       sv1[buf] = 0;
     }
   };
-  load_unit(0, 0);
+  load_from(unit_addr(0), 0);
 
   // 3) x split into records in this wave's tile (before it holds weights), then the
   //    A operands of the slice's 4 chunks into registers, kept for the pass.
@@ -279,7 +292,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   };
   prep(xr[0]);
 #pragma unroll
-  for (int d = 1; d < D; ++d) load_unit(d, d);
+  for (int d = 1; d < D; ++d) load_from(unit_addr(d), d);
 
   // sum the waves' partials of row blocks [rb_first, rb_last] in wave order
   auto flush = [&](int rb_first, int rb_last) __attribute__((always_inline)) {
@@ -322,7 +335,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
         *(uint2 *)(st + 8 * lane) = make_uint2(sv0[d], sv1[d]);
       else
         *(uint32_t *)(st + 4 * lane) = sv0[d];
-      load_unit(p * uppd + r + D, d);
+      load_from(unit_addr(p * uppd + r + D), d);
       const bool live = r < upp;
       // a slice past K (last pass only) re-read the last slice: its sums are dropped
       const bool real = P == 1 || p * Q + q < S;
@@ -637,6 +650,8 @@ bool qmv_mfma_ok(const QmmArgs &a) {
   if (g.P > 1 && (qf_cus() == 0 || qf_flush_rows(a, qf_nrb(a, qf_cus())) < qf_nrb(a, qf_cus()))) return false;
   if ((((uintptr_t)a.x) | ((uintptr_t)a.w)) & 15) return false;
   if (((uintptr_t)a.s) & 7) return false;  // scale slices are read as 8 (nvfp4) / 4 (mxfp8) bytes
+  // W and scale addresses are 32-bit offsets within the matrix
+  if ((int64_t)a.N * (a.mode == NVFP4 ? a.K / 2 : a.K) >= ((int64_t)1 << 32)) return false;
   return true;
 }
 
