@@ -226,9 +226,9 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   auto wbase = [&](int i) __attribute__((always_inline)) {
     return NMAT == 2 && RPL * i >= 8 ? w2 : w;  // a load's rows are all in one matrix
   };
-  auto unit_addr = [&](int u) __attribute__((always_inline)) {
-    const int pass = P == 1 ? 0 : u / uppd, rb = u - pass * uppd;
-    const int sl = slice_of(pass < P ? pass : P - 1);
+  // unit (pass, rb); row blocks past the range read clamped rows (unused)
+  auto unit_addr = [&](int pass, int rb) __attribute__((always_inline)) {
+    const int sl = slice_of(pass);
     const int wcol = sl * G::UB + 16 * (lane % LPR), scol = sl * G::SB + (lane & 3) * (G::SB / 4);
     UnitAddr a;
 #pragma unroll
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
       sv1[buf] = 0;
     }
   };
-  load_from(unit_addr(0), 0);
+  load_from(unit_addr(0, 0), 0);
 
   // 3) x split into records in this wave's tile (before it holds weights), then the
   //    A operands of the slice's 4 chunks into registers, kept for the pass.
@@ -292,7 +292,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   };
   prep(xr[0]);
 #pragma unroll
-  for (int d = 1; d < D; ++d) load_from(unit_addr(d), d);
+  for (int d = 1; d < D; ++d) load_from(unit_addr(0, d), d);
 
   // sum the waves' partials of row blocks [rb_first, rb_last] in wave order
   auto flush = [&](int rb_first, int rb_last) __attribute__((always_inline)) {
@@ -300,8 +300,9 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
     const int items = (rb_last - rb_first + 1) * M * RB;
     for (int t = tid; t < items; t += 64 * Q) {
       const int nn = t % RB, m = (t / RB) % M, rbi = t / (RB * M);
-      const int rb = rb_first + rbi, row = r_begin + RB * rb + nn;
-      const float *pp = part + (((rb % F) * M + m) * Q) * 16 + nn;
+      // rb_first is a multiple of F: row block rb_first + rbi sits in slot rbi
+      const int row = r_begin + RB * (rb_first + rbi) + nn;
+      const float *pp = part + ((rbi * M + m) * Q) * 16 + nn;
       float sum[NMAT];
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat) {
@@ -322,6 +323,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
    // units go in groups of D so that buffer indices are static; the units past
    // the last one are computed too (clamped rows): loads and MFMAs under a branch
    // make the compiler's wait counting conservative.
+   int rbf = 0;  // rb % F, kept by a counter (no division in the loop)
    for (int r0 = 0; r0 < uppd; r0 += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
@@ -335,11 +337,13 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
         *(uint2 *)(st + 8 * lane) = make_uint2(sv0[d], sv1[d]);
       else
         *(uint32_t *)(st + 4 * lane) = sv0[d];
-      load_from(unit_addr(p * uppd + r + D), d);
+      // unit r + D of this pass, or of the next one (a select, not a division); after
+      // the last pass's last unit the clamped rows of this pass (one row, cached)
+      const bool wrap = p + 1 < P && r + D >= uppd;
+      load_from(unit_addr(wrap ? p + 1 : p, wrap ? r + D - uppd : r + D), d);
       const bool live = r < upp;
       // a slice past K (last pass only) re-read the last slice: its sums are dropped
       const bool real = P == 1 || p * Q + q < S;
-      const int rbf = rb % F;
       float *pslot = part + (rbf * M) * Q * 16;
       if constexpr (MODE == NVFP4) {
         float acc[M];
@@ -399,7 +403,8 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
         for (int c = 0; c < 4; ++c) keep_live(bsc[c]);
       }
       // with several passes the host sets F >= nrb: one flush, after the last pass
-      if (live && p == P - 1 && ((rb + 1) % F == 0 || rb + 1 == nrb)) flush(rb - rbf, rb);
+      if (live && p == P - 1 && (rbf + 1 == F || rb + 1 == nrb)) flush(rb - rbf, rb);
+      rbf = rbf + 1 == F ? 0 : rbf + 1;
     }
    }
   }
@@ -468,18 +473,20 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
     return row < r_end ? row : r_end - 1;  // rows past the range re-read its last row (results dropped)
   };
   uint4 wv[8], sv;
-  auto load_unit = [&](int u) __attribute__((always_inline)) {
-    const int pass = u / nrb, rb = u - pass * nrb;
-    const int sl = slice_of(pass < P ? pass : P - 1);
+  // unit (pass, rb); row blocks past the range read clamped rows (unused).
+  // W and scale addresses are 32-bit offsets (the host checks that a matrix is under 4 GiB).
+  const uint8_t *sbase = NMAT == 2 && lane >= 32 ? s2 : s;  // this lane's scale rows
+  auto load_unit = [&](int pass, int rb) __attribute__((always_inline)) {
+    const int sl = slice_of(pass);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint8_t *wm = NMAT == 2 && i >= 4 ? w2 : w;  // a load's rows are all in one matrix
-      wv[i] = load_stream16(wm + row_of(rb, 4 * i + (lane >> 4)) * wrow + sl * 256 + 16 * (lane & 15));
+      wv[i] = load_stream16(wm + ((uint32_t)row_of(rb, 4 * i + (lane >> 4)) * (uint32_t)wrow + sl * 256 +
+                                  16 * (lane & 15)));
     }
-    const uint8_t *sm = NMAT == 2 && lane >= 32 ? s2 : s;
-    sv = *(const uint4 *)(sm + row_of(rb, lane >> 1) * srow + sl * 32 + 16 * (lane & 1));
+    sv = *(const uint4 *)(sbase + ((uint32_t)row_of(rb, lane >> 1) * (uint32_t)srow + sl * 32 + 16 * (lane & 1)));
   };
-  load_unit(0);
+  load_unit(0, 0);
 
   // A operands of the slice's 8 chunks (see above), from the x records
   const int i = lane & 31, h = lane >> 5;
@@ -508,8 +515,9 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
     const int items = (rb_last - rb_first + 1) * M * RB;
     for (int t = tid; t < items; t += 64 * Q) {
       const int nn = t % RB, m = (t / RB) % M, rbi = t / (RB * M);
-      const int rb = rb_first + rbi, row = r_begin + RB * rb + nn;
-      const float *pp = part + (((rb % F) * M + m) * Q) * 64 + nn;
+      // rb_first is a multiple of F: row block rb_first + rbi sits in slot rbi
+      const int row = r_begin + RB * (rb_first + rbi) + nn;
+      const float *pp = part + ((rbi * M + m) * Q) * 64 + nn;
       float sum[NMAT];
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat) {
@@ -532,14 +540,17 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
     const bool real = P == 1 || p * Q + q < S;
     // a do-while: every workgroup has a row block, and the compiler then counts the
     // next pass's x loads as older than the unit loads (exact wait before the split)
-    int rb = 0;
+    int rb = 0, rbf = 0;  // rbf = rb % F, kept by a counter (no division in the loop)
     do {
       // unit (p, rb): registers -> tile (the x records are no longer needed there), then
       // refill the registers with the next unit (past the last one: clamped, unused)
 #pragma unroll
       for (int li = 0; li < 8; ++li) *(uint4 *)(wt + (4 * li + (lane >> 4)) * Q32_PITCH + 16 * (lane & 15)) = wv[li];
       *(uint4 *)(st + 16 * lane) = sv;
-      load_unit(p * nrb + rb + 1);
+      // the next unit: this pass's next row block or the next pass's first; after the
+      // last pass's last unit the clamped rows past the range (one row, cached)
+      const bool wrap = p + 1 < P && rb + 1 >= nrb;
+      load_unit(wrap ? p + 1 : p, wrap ? 0 : rb + 1);
       float acc[M];
 #pragma unroll
       for (int m = 0; m < M; ++m) acc[m] = 0.f;
@@ -569,7 +580,6 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
       }
       // every lane stores its half's sums (no branch: the compiler would sink the
       // accumulation of rows m > 0 into it and keep all chunks' outputs live)
-      const int rbf = rb % F;
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         float *dst = part + ((rbf * M + m) * Q + q) * 64 + lane;
@@ -579,7 +589,8 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
 #pragma unroll
       for (int c8 = 0; c8 < 8; ++c8) keep_live(asreg[c8]);
       // with several passes the host sets F >= nrb: one flush, after the last pass
-      if (p == P - 1 && ((rb + 1) % F == 0 || rb + 1 == nrb)) flush(rb - rbf, rb);
+      if (p == P - 1 && (rbf + 1 == F || rb + 1 == nrb)) flush(rb - rbf, rb);
+      rbf = rbf + 1 == F ? 0 : rbf + 1;
     } while (++rb < nrb);
   }
 }
@@ -752,6 +763,7 @@ static bool q32_ok(const QmmArgs &a) {
   const QfShape g = qf_shape(a.K);
   if (g.Q == 0 || qf_cus() == 0) return false;
   if (g.P > 1 && q32_flush_rows(a, q32_nrb(a, qf_cus())) < q32_nrb(a, qf_cus())) return false;
+  if ((int64_t)a.N * (a.K / 2) >= ((int64_t)1 << 32)) return false;  // 32-bit offsets within W
   return ((((uintptr_t)a.x) | ((uintptr_t)a.w) | ((uintptr_t)a.s)) & 15) == 0;
 }
 
