@@ -201,6 +201,9 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
   for (int p = 0; p < P; ++p)
 #pragma unroll
     for (int m = 0; m < M; ++m) xr[p][m] = *(const uint4 *)(x + (int64_t)m * K + 512 * slice_of(p) + 8 * lane);
+  // x goes out before the weights: a later x load would make the first split wait for
+  // the first unit's loads too (the wait counter counts in issue order)
+  __builtin_amdgcn_sched_barrier(0);
 
   // 2) the first unit's weights.  Load i, lane l: nvfp4 row 4i + l/16, bytes 16 (l%16);
   //    mxfp8 row 2i + l/32, bytes 16 (l%32).  Scales: lane l, row l/4, bytes (l%4) SB/4.
@@ -212,8 +215,8 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
     const int row = r_begin + RB * rb + (NMAT == 2 ? (rr & 7) : rr);
     return row < r_end ? row : r_end - 1;  // rows past the range re-read its last row (results dropped)
   };
-  // unit u = (pass u / uppd, row block u % uppd) lives in buffer u % D; units past a
-  // pass's last row block load clamped rows and are not stored
+  // unit (pass, row block r) lives in buffer r % D; units past a pass's last row
+  // block load clamped rows and are not stored
   uint4 wv[D][G::LOADS];
   uint32_t sv0[D], sv1[D];
   // W addresses are 32-bit offsets from the matrix base (the host checks that a
@@ -322,9 +325,12 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
    if (p > 0) prep(xr[p]);
    // units go in groups of D so that buffer indices are static; the units past
    // the last one are computed too (clamped rows): loads and MFMAs under a branch
-   // make the compiler's wait counting conservative.
+   // make the compiler's wait counting conservative.  A do-while: every workgroup
+   // has a row block, and the compiler then counts the next pass's x loads as
+   // older than the unit loads (an exact wait before the split, not vmcnt(0)).
    int rbf = 0;  // rb % F, kept by a counter (no division in the loop)
-   for (int r0 = 0; r0 < uppd; r0 += D) {
+   int r0 = 0;
+   do {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int r = r0 + d, rb = r;
@@ -406,7 +412,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
       if (live && p == P - 1 && (rbf + 1 == F || rb + 1 == nrb)) flush(rb - rbf, rb);
       rbf = rbf + 1 == F ? 0 : rbf + 1;
     }
-   }
+   } while ((r0 += D) < uppd);
   }
 }
 
@@ -464,7 +470,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
   };
   load_x(0);
 
-  // unit u = (pass u / nrb, row block u % nrb).  Load i, lane l: row 4i + l/16,
+  // unit (pass, row block rb).  Load i, lane l: row 4i + l/16,
   // bytes 16 (l%16) of the slice; scales: lane l, row l/2, bytes 16 (l%2).
   const int64_t wrow = K >> 1, srow = K >> 4;
   // unit row rr of row block rb (NMAT = 2: rr < 16 in W, rr >= 16 the same rows in W2)
