@@ -70,6 +70,32 @@ CONFIGS = {
                                  "Dk=Dv=128, bf16 q/k/v/beta, f32 g and state"),
 }
 DEFAULT = "gateup"
+
+# Every quantized linear of one decoded token at the model's default sizes
+# (H=5120, I=17408, V=248320; src/model.zig:40-59): (weight, N, K, calls per
+# token, call site).  48 GDN layers and 16 full-attention layers.
+CENSUS = [
+    ("self_attn.q_proj", 12288, 5120, 16, "src/model.zig:929"),
+    ("self_attn.k_proj", 1024, 5120, 16, "src/model.zig:940"),
+    ("self_attn.v_proj", 1024, 5120, 16, "src/model.zig:944"),
+    ("self_attn.o_proj", 5120, 6144, 16, "src/model.zig:979"),
+    ("linear_attn.in_proj_qkv", 10240, 5120, 48, "src/model.zig:1066"),
+    ("linear_attn.in_proj_z", 6144, 5120, 48, "src/model.zig:1068"),
+    ("linear_attn.in_proj_b", 48, 5120, 48, "src/model.zig:1072"),
+    ("linear_attn.in_proj_a", 48, 5120, 48, "src/model.zig:1074"),
+    ("linear_attn.out_proj", 5120, 6144, 48, "src/model.zig:1230"),
+    ("mlp.gate_proj", 17408, 5120, 64, "src/model.zig:906"),
+    ("mlp.up_proj", 17408, 5120, 64, "src/model.zig:908"),
+    ("mlp.down_proj", 5120, 17408, 64, "src/model.zig:914"),
+    ("lm_head", 248320, 5120, 1, "src/model.zig:1309"),
+    ("mtp.fc", 5120, 10240, 0, "src/mtp.zig:158"),  # MTP drafting only: not in the per-token sum
+]
+# Projections of one x that a grouped call runs as one matrix (the loader places them back to back).
+CENSUS_GROUPS = {
+    "linear_attn.in_proj_qkv+z+b+a (grouped)": ("linear_attn.in_proj_qkv", "linear_attn.in_proj_z",
+                                                "linear_attn.in_proj_b", "linear_attn.in_proj_a"),
+    "self_attn.q+k+v_proj (grouped)": ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"),
+}
 BITS = {"mxfp8": 8, "nvfp4": 4, "bf16": 16}
 GROUP = {"mxfp8": 32, "nvfp4": 16, "bf16": None}
 ROTATE_BYTES = 512 << 20
@@ -258,6 +284,135 @@ def bench_gdn(args, cfg):
     print(json.dumps(line), flush=True)
 
 
+def bench_census(args):
+    """Time every call-site shape of one decoded token (CENSUS) in one mode at M rows.
+
+    Each shape's quantized weights are replicated at 256-byte aligned offsets of one
+    buffer of >= 512 MiB (one copy if larger), so every timed call reads cold weights
+    even for the 48-row projections.  mxfp8 checkpoints keep lm_head dense bf16
+    (src/model.zig:215-216), so in mxfp8 mode lm_head runs the dense GEMV.  Prints one
+    JSON line: per-shape us, GB/s and fraction of HBM peak, and the per-token sums with
+    gate and up as two calls or as the fused gate+up+SiLU*mul call."""
+    import numpy as np
+    import torch
+
+    import qmm as Q
+
+    mode, M = args.census, args.census_m
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    stream = Q.Stream.torch_current()
+    al = lambda n: (n + 255) // 256 * 256
+    gen.manual_seed(7)
+    x_full = (torch.randn((M, 17408), generator=gen, device=dev, dtype=torch.float32)).to(torch.bfloat16)
+    rows = [(name, N, K, calls, site, False, None) for name, N, K, calls, site in CENSUS]
+    rows.append(("mlp.gate_up_silu (fused gate+up)", 17408, 5120, 64, "src/model.zig:905-915", True, None))
+    # grouped projections of one x (qmm_quantized_matmul_group), members back to back
+    for gname, members in CENSUS_GROUPS.items():
+        parts = [r for r in CENSUS if r[0] in members]
+        rows.append((gname, sum(r[1] for r in parts), parts[0][2], parts[0][3],
+                     ", ".join(r[4] for r in parts), False, [r[1] for r in parts]))
+    results = []
+    for name, N, K, calls, site, fused, group in rows:
+        m = "bf16" if (mode == "mxfp8" and name == "lm_head") else mode
+        gen.manual_seed(1000 + N + K)
+        W = (torch.randn((N, K), generator=gen, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+        if m == "bf16":
+            parts = [W.contiguous().view(torch.uint8).view(-1)]
+        else:
+            wq, sc = Q.quantize(Q.Array.from_torch(W), m, stream=stream)
+            torch.cuda.synchronize()
+            parts = [torch.from_numpy(a.numpy().view(np.uint8).reshape(-1)).to(dev) for a in (wq, sc)]
+            del wq, sc
+        del W
+        sizes = [p.numel() for p in parts]
+        per = sum(al(s) for s in sizes)
+        copies = max(2 if fused else 1, math.ceil(ROTATE_BYTES / per))
+        buf = torch.empty(copies * per, dtype=torch.uint8, device=dev)
+        mats, tmats = [], []
+        for c in range(copies):
+            off, views = c * per, []
+            for p, s in zip(parts, sizes):
+                buf[off:off + s].copy_(p)
+                views.append(buf[off:off + s])
+                off += al(s)
+            if m == "bf16":
+                mats.append((Q.Array.from_torch(views[0].view(torch.bfloat16).view(N, K)),))
+            else:
+                wcols = K * BITS[m] // 32
+                tmats.append((views[0].view(torch.int32).view(N, wcols), views[1].view(N, K // GROUP[m])))
+                mats.append((Q.Array.from_torch(tmats[-1][0], dtype=Q.UINT32), Q.Array.from_torch(tmats[-1][1])))
+        del parts
+        x = Q.Array.from_torch(x_full[:, :K].contiguous())
+        yt = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        y = Q.Array.from_torch(yt)
+        torch.cuda.synchronize()
+
+        if group:
+            # each copy's members: row slices of the copy (back to back, as the loader places them)
+            gmats, outs = [], [Q.Array.from_torch(torch.empty((M, n), dtype=torch.bfloat16, device=dev))
+                               for n in group]
+            for wt_, st_ in tmats:
+                ws_, ss_, r0 = [], [], 0
+                for n in group:
+                    ws_.append(Q.Array.from_torch(wt_[r0:r0 + n], dtype=Q.UINT32))
+                    ss_.append(Q.Array.from_torch(st_[r0:r0 + n]))
+                    r0 += n
+                gmats.append((ws_, ss_))
+
+        def step(i, st):
+            if group:
+                ws_, ss_ = gmats[i % copies]
+                Q.quantized_matmul_group(x, ws_, ss_, m, outs=outs, stream=st)
+            elif fused:
+                (wg, sg), (wu, su) = mats[i % copies], mats[(i + 1) % copies]
+                Q.mlp_gate_up_silu(x, wg, sg, wu, su, m, out=y, stream=st)
+            elif m == "bf16":
+                Q.linear(x, mats[i % copies][0], out=y, stream=st)
+            else:
+                wq_, sc_ = mats[i % copies]
+                Q.quantized_matmul(x, wq_, sc_, m, out=y, stream=st)
+
+        for i in range(args.warmup):
+            step(i, stream)
+        torch.cuda.synchronize()
+        ms = replay_timed(step, args.steps)
+        cfg = dict(mode=m, M=M, N=N, K=K, mlp=fused)
+        alg = algorithmic(cfg)
+        gbs = alg["bytes"] / (ms / 1e3) / 1e9
+        results.append(dict(weight=name, site=site, mode=m, N=N, K=K, calls_per_token=calls,
+                            us=round(ms * 1e3, 2), gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4),
+                            bytes=alg["bytes"], copies=copies))
+        print(f"[census] {name:34s} {m:5s} N={N:6d} K={K:5d} M={M}: {ms * 1e3:8.2f} us {gbs:7.1f} GB/s "
+              f"({gbs / HBM_PEAK_GBS:.3f})", file=sys.stderr, flush=True)
+        del mats, tmats, buf, x, y, yt
+        if group:
+            del gmats, outs
+        torch.cuda.empty_cache()
+    extra = ("mlp.gate_up_silu",) + tuple(CENSUS_GROUPS)
+    base = [r for r in results if not r["weight"].startswith(extra)]
+    by = {r["weight"]: r for r in results}
+    us_sep = sum(r["us"] * r["calls_per_token"] for r in base)
+    bytes_sep = sum(r["bytes"] * r["calls_per_token"] for r in base)
+    cost = lambda names: sum(by[n]["us"] * by[n]["calls_per_token"] for n in names)
+    us_fused = us_sep - cost(("mlp.gate_proj", "mlp.up_proj")) + cost(("mlp.gate_up_silu (fused gate+up)",))
+    us_grouped = us_fused
+    for gname, members in CENSUS_GROUPS.items():
+        us_grouped += cost((gname,)) - cost(members)
+    line = {
+        "census": mode, "M": M, "steps": args.steps, "timing": "hip graph replay per shape",
+        "data": "synthetic (seeded N(0,1) x, N(0,0.02) W quantized on device)",
+        "shapes": results,
+        "per_token": {"calls": sum(r["calls_per_token"] for r in base), "weight_bytes": bytes_sep,
+                      "us_separate": round(us_sep, 1), "us_mlp_fused": round(us_fused, 1),
+                      "us_mlp_fused_and_grouped": round(us_grouped, 1),
+                      "gbs_separate": round(bytes_sep / us_sep / 1e3, 1),
+                      "gbs_mlp_fused_and_grouped": round(bytes_sep / us_grouped / 1e3, 1)},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -266,6 +421,9 @@ def main():
     ap.add_argument("--config", default=DEFAULT, choices=sorted(CONFIGS))
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--census", choices=("nvfp4", "mxfp8"),
+                    help="instead of one config, time every quantized linear of a decoded token in this mode")
+    ap.add_argument("--census-m", type=int, default=1, help="x rows for --census (1 decode, 2-3 MTP verify)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the workload, run K plain 512 MiB -> 512 MiB copy kernels (torch.neg on "
                          "float32) so HBM counters (FETCH_SIZE / WRITE_SIZE) can be scaled to known bytes")
@@ -292,6 +450,8 @@ def main():
                           "bytes_written_per_launch": n * 4, "launches": args.steps}), flush=True)
         return
 
+    if args.census:
+        return bench_census(args)
     cfg = CONFIGS[args.config]
     if cfg.get("gdn"):
         return bench_gdn(args, cfg)

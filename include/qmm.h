@@ -91,6 +91,21 @@ int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array sca
                          bool transpose_w, qmm_optional_int group_size, qmm_optional_int bits,
                          const char *mode, qmm_stream s);
 
+/* res[i] = x @ deq(w[i]).T for i < n (1 <= n <= 4): projections of one x with the
+ * same K and mode, each argument as in qmm_quantized_matmul (res[i] written in
+ * place when it holds an array of the output shape).  Replaces n consecutive
+ * qlinear calls on one x: the GDN layer's in_proj_qkv / z / b / a
+ * (src/model.zig:1066-1074) and attention's q / k / v (:929-944).  When the
+ * matrices lie back to back in memory, and so do their scales (in any order;
+ * qmm_weights_load places each layer's groups so), and M <= 4 with bfloat16 x,
+ * one kernel runs over them as one matrix; otherwise one call per matrix.  Either
+ * way res[i] meets the bar of qmm_quantized_matmul(x, w[i], scales[i]); the one
+ * launch picks its kernel by the total row count, which can differ from the
+ * single call's choice, so the bf16 roundings of the two may differ. */
+int qmm_quantized_matmul_group(qmm_array *res, size_t n, qmm_array x, const qmm_array *w, const qmm_array *scales,
+                               qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
+                               qmm_stream s);
+
 /* deq(w) as [N, K] of `dtype` (default bfloat16; float32 and bfloat16 supported)
  * (src/mlx.zig:274).  biases and global_scale must be null handles. */
 int qmm_dequantize(qmm_array *res, qmm_array w, qmm_array scales, qmm_array biases,
@@ -162,6 +177,8 @@ void qmm_reset_faults_for_test(void);
 void qmm_fault_arm(uint64_t k);
 bool qmm_fault_did_fire(void);
 uint64_t qmm_op_count(void);
+/* Grouped calls (qmm_quantized_matmul_group) that ran as one kernel launch (diagnostics). */
+uint64_t qmm_group_launch_count(void);
 
 /* ---- weights (src/weights.zig) ---- */
 typedef enum { QMM_QUANT_NONE = 0, QMM_QUANT_MXFP8 = 1, QMM_QUANT_NVFP4 = 2 } qmm_quant_mode;
@@ -191,7 +208,11 @@ int qmm_parse_header_json(const char *json, size_t len, size_t *n_tensors);
 int qmm_sanitize_name(const char *name, char *out, size_t out_len);
 
 /* Load a sharded safetensors checkpoint (model.safetensors.index.json + shards)
- * into HBM, tensors copied raw from their data_offsets (WeightMap.load, :257-352). */
+ * into HBM, tensors copied raw from their data_offsets (WeightMap.load, :257-352).
+ * The packed weights of each layer's linear_attn.in_proj_{qkv,z,b,a},
+ * self_attn.{q,k,v}_proj and mlp.{gate,up}_proj are placed back to back in that
+ * order (and their scales likewise) when every member is present and all but the
+ * last are multiples of 256 bytes, for qmm_quantized_matmul_group. */
 int qmm_weights_load(qmm_weight_map *res, const char *model_dir, qmm_stream s);
 int qmm_weights_free(qmm_weight_map m);
 /* Borrowed handle (do not free), or a NULL ctx when absent (WeightMap.get). */
@@ -205,6 +226,11 @@ qmm_quant_spec qmm_weights_quant(qmm_weight_map m);
  * linear (src/model.zig:200-211); U32 weight without scales or a name not ending
  * in ".weight" -> QMM_WE_MISSING_WEIGHT. */
 int qmm_named_linear_q(qmm_array *res, qmm_weight_map m, qmm_array x, const char *name, qmm_stream s);
+/* n <= 4 projections of one x by checkpoint name (layerLinearQ calls on one x,
+ * src/model.zig:1066-1074 and :929-944): qmm_quantized_matmul_group when every
+ * weight is packed with scales, else qmm_named_linear_q per name. */
+int qmm_named_linear_q_group(qmm_array *res, size_t n, qmm_weight_map m, qmm_array x, const char *const *names,
+                             qmm_stream s);
 /* Dense y = x @ w.T for bf16 x [..., M, K] and bf16 w [N, K] (linear, src/model.zig:200-211). */
 int qmm_linear(qmm_array *res, qmm_array x, qmm_array w, qmm_stream s);
 /* mlpForwardQ (src/model.zig:905-915): down(silu(gate(x)) * up(x)) by checkpoint

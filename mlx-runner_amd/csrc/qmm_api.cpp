@@ -2,6 +2,7 @@
 // mlx-runner's quantized linear path binds (src/mlx.zig:265, :274, :278).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -516,6 +517,103 @@ int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array sca
   a.s = (const uint8_t *)sa->data;
   a.y = ya->data;
   if (run_qmm(a, ya->nbytes(), st, op)) return finish(1);
+  return finish(0);
+}
+
+// n projections of one x (the GDN layer's in_proj_qkv / z / b / a, src/model.zig:
+// 1066-1074; attention's q / k / v, :929-944).  When the matrices, and their
+// scales, lie back to back in memory (in any order) and the shape is a decode
+// shape, one kernel runs over them as one matrix and writes each part's rows to
+// its own result.
+static std::atomic<uint64_t> g_group_launches{0};
+uint64_t qmm_group_launch_count(void) { return g_group_launches.load(std::memory_order_relaxed); }
+
+int qmm_quantized_matmul_group(qmm_array *res, size_t n, qmm_array x, const qmm_array *w, const qmm_array *scales,
+                               qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
+                               qmm_stream s) {
+  const char *op = "quantized_matmul_group";
+  if (!res || !w || !scales) return finish(fail("[%s] null argument", op));
+  if (n < 1 || n > 4) return finish(fail("[%s] takes 1 to 4 matrices, got %zu", op, n));
+  int m;
+  if (parse_mode(mode, group_size, bits, op, &m)) return finish(1);
+  Arr *xa = (Arr *)x.ctx;
+  if (!xa) return finish(fail("[%s] missing x", op));
+  if (xa->dtype != QMM_BFLOAT16 && xa->dtype != QMM_FLOAT32)
+    return finish(fail("[%s] x must be bfloat16 or float32", op));
+  if (xa->ndim < 1) return finish(fail("[%s] x must have at least one dimension", op));
+  int N[4], K = 0;
+  for (size_t i = 0; i < n; ++i) {
+    int Ki;
+    if (check_wq((Arr *)w[i].ctx, (Arr *)scales[i].ctx, m, op, &N[i], &Ki)) return finish(1);
+    if (i > 0 && Ki != K) return finish(fail("[%s] matrix %zu has K = %d, matrix 0 has %d", op, i, Ki, K));
+    K = Ki;
+  }
+  if (xa->shape[xa->ndim - 1] != K)
+    return finish(fail("[%s] Last dimension of x (%d) does not match the weights' K (%d)", op,
+                       xa->shape[xa->ndim - 1], K));
+  int64_t M = 1;
+  for (int i = 0; i < xa->ndim - 1; ++i) M *= xa->shape[i];
+  if (M > INT32_MAX) return finish(fail("[%s] too many rows", op));
+  hipStream_t st = stream_of(s);
+  Arr *ya[4];
+  for (size_t i = 0; i < n; ++i) {
+    std::vector<int> oshape(xa->shape, xa->shape + xa->ndim);
+    oshape.back() = N[i];
+    if (alloc_arr(&res[i], oshape, xa->dtype, st, &ya[i])) return finish(1);
+  }
+  if (M == 0) return finish(0);
+  QmmArgs a;
+  a.mode = m;
+  a.x_f32 = xa->dtype == QMM_FLOAT32;
+  a.M = (int)M;
+  a.K = K;
+  a.x = xa->data;
+  // back to back: sorted by address, each matrix starts where the previous one ends
+  int ord[4] = {0, 1, 2, 3};
+  std::sort(ord, ord + n, [&](int i, int j) { return ((Arr *)w[i].ctx)->data < ((Arr *)w[j].ctx)->data; });
+  const int64_t wrow = m == MXFP8 ? K : K / 2, srow = K / (m == MXFP8 ? 32 : 16);
+  const uint8_t *w0 = (const uint8_t *)((Arr *)w[ord[0]].ctx)->data;
+  const uint8_t *s0 = (const uint8_t *)((Arr *)scales[ord[0]].ctx)->data;
+  bool together = K > 0;
+  int64_t rows = 0;
+  QmmParts parts;
+  parts.n = (int)n;
+  for (size_t j = 0; j < n; ++j) {
+    const int i = ord[j];
+    together = together && N[i] > 0 && (const uint8_t *)((Arr *)w[i].ctx)->data == w0 + rows * wrow &&
+               (const uint8_t *)((Arr *)scales[i].ctx)->data == s0 + rows * srow;
+    parts.y[j] = ya[i]->data;
+    parts.rows[j] = N[i];
+    rows += N[i];
+  }
+  if (together && rows <= INT32_MAX) {
+    a.N = (int)rows;
+    a.w = w0;
+    a.s = s0;
+    a.y = nullptr;
+    a.parts = &parts;
+    if (qmv_parts_ok(a)) {
+      const hipError_t e = qmv_mfma_ok(a) ? launch_qmv_mfma(a, st) : launch_qmv(a, st);
+      if (e != hipSuccess) return finish(fail_hip(e, op));
+      g_group_launches.fetch_add(1, std::memory_order_relaxed);
+      return finish(0);
+    }
+  }
+  // otherwise one call per matrix
+  for (size_t i = 0; i < n; ++i) {
+    if (N[i] == 0) continue;
+    QmmArgs b;
+    b.mode = m;
+    b.x_f32 = a.x_f32;
+    b.M = (int)M;
+    b.N = N[i];
+    b.K = K;
+    b.x = xa->data;
+    b.w = (const uint8_t *)((Arr *)w[i].ctx)->data;
+    b.s = (const uint8_t *)((Arr *)scales[i].ctx)->data;
+    b.y = ya[i]->data;
+    if (run_qmm(b, ya[i]->nbytes(), st, op)) return finish(1);
+  }
   return finish(0);
 }
 

@@ -9,6 +9,29 @@ enum Mode : int { MXFP8 = 0, NVFP4 = 1 };
 
 constexpr int QMV_MAX_M = 8;  // rows of x served by the decode (GEMV / skinny) kernels
 
+// Where the decode kernels write output row r of y[M, N]: one bf16 array [M, N],
+// or (a grouped call: several weight matrices of one K that share x and lie back
+// to back in memory, run as one matrix) up to 4 arrays, row r in [lo_i, lo_(i+1))
+// going to array i, an [M, n_i] row-major array, at row r - lo_i.
+struct YOut {
+  uint16_t *y0, *y1, *y2, *y3;
+  int lo1, lo2, lo3;   // first row of parts 1..3 (INT32_MAX when absent)
+  int n0, n1, n2, n3;  // rows of each part
+  __host__ __device__ __forceinline__ uint16_t *at(int m, int r) const {
+    if (r >= lo3) return y3 + (int64_t)m * n3 + (r - lo3);
+    if (r >= lo2) return y2 + (int64_t)m * n2 + (r - lo2);
+    if (r >= lo1) return y1 + (int64_t)m * n1 + (r - lo1);
+    return y0 + (int64_t)m * n0 + r;
+  }
+};
+
+// The parts of a grouped call's output (host side): part i has rows[i] rows.
+struct QmmParts {
+  int n;           // 1..4
+  void *y[4];
+  int rows[4];
+};
+
 struct QmmArgs {
   int mode;        // 0 = mxfp8, 1 = nvfp4
   bool x_f32;      // x (and y) float32 instead of bfloat16
@@ -17,7 +40,31 @@ struct QmmArgs {
   const uint8_t *w;  // packed rows, K*bits/8 bytes each
   const uint8_t *s;  // scale bytes, K/group per row
   void *y;
+  const QmmParts *parts = nullptr;  // a grouped call's outputs (then y is unused)
 };
+
+// The output descriptor of a call: y as one part, or the grouped call's parts.
+inline YOut yout_of(const QmmArgs &a) {
+  YOut o{(uint16_t *)a.y, nullptr, nullptr, nullptr, INT32_MAX, INT32_MAX, INT32_MAX, a.N, 0, 0, 0};
+  if (!a.parts) return o;
+  const QmmParts &p = *a.parts;
+  uint16_t **ys[4] = {&o.y0, &o.y1, &o.y2, &o.y3};
+  int *los[4] = {nullptr, &o.lo1, &o.lo2, &o.lo3};
+  int *ns[4] = {&o.n0, &o.n1, &o.n2, &o.n3};
+  int lo = 0;
+  for (int i = 0; i < p.n && i < 4; ++i) {
+    *ys[i] = (uint16_t *)p.y[i];
+    if (i > 0) *los[i] = lo;
+    *ns[i] = p.rows[i];
+    lo += p.rows[i];
+  }
+  return o;
+}
+
+// Whether the decode kernels that take a YOut serve these arguments (the grouped
+// call's one-launch path; other shapes run one call per matrix).
+bool qmv_parts_ok(const QmmArgs &a);
+bool qmv_mfma_parts_ok(const QmmArgs &a);
 
 bool qmv_fast_ok(const QmmArgs &a);
 hipError_t launch_qmv(const QmmArgs &a, hipStream_t st);

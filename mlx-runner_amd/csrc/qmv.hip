@@ -236,11 +236,11 @@ constexpr size_t QMV_LDS_MAX = 64 * 1024;
 
 // MLP: the wave's two rows are row n of W (gate) and row n of W2 (up), and the
 // output is silu(gate) * up with the reference's bf16 roundings (silu_mul_bf16).
-template <int MODE, int M, int R, int ISEG, int XP, bool DB, bool MLP = false>
+template <int MODE, int M, int R, int ISEG, int XP, bool DB, bool MLP = false, bool PARTS = false>
 __global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t *__restrict__ x,
                                                                   const uint8_t *__restrict__ w,
                                                                   const uint8_t *__restrict__ s,
-                                                                  uint16_t *__restrict__ y, int N, int K,
+                                                                  const YOut yo, int N, int K,
                                                                   const uint8_t *__restrict__ w2 = nullptr,
                                                                   const uint8_t *__restrict__ s2 = nullptr) {
   using L = XLayout<MODE>;
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t
       const float g = wave_sum(acc[0][m]), u = wave_sum(acc[1][m]);
       out = (lane == m) ? silu_mul_bf16(g, u) : out;
     }
-    if (lane < M && n0 < N) y[(int64_t)lane * N + n0] = f32_to_bf16_rne(out);
+    if (lane < M && n0 < N) yo.y0[(int64_t)lane * N + n0] = f32_to_bf16_rne(out);
     return;
   }
   float out = 0.f;
@@ -432,11 +432,17 @@ __global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t
     }
   if (lane < R * M) {
     const int r = lane / M, m = lane % M;
-    if (n0 + r < N) y[(int64_t)m * N + n0 + r] = f32_to_bf16_rne(out);
+    if (n0 + r < N) {
+      const uint16_t v = f32_to_bf16_rne(out);
+      if constexpr (PARTS)
+        *yo.at(m, n0 + r) = v;
+      else
+        yo.y0[(int64_t)m * N + n0 + r] = v;
+    }
   }
 }
 
-template <int MODE, int M, int R, int ISEG, bool DB>
+template <int MODE, int M, int R, int ISEG, bool DB, bool PARTS = false>
 static hipError_t launch_qmv_bf16_t(const QmmArgs &a, hipStream_t st) {
   const size_t lds = qmv_lds_bytes(MODE, M, a.K);
   const int C = MODE == MXFP8 ? a.K / 16 : a.K / 32;
@@ -444,13 +450,16 @@ static hipError_t launch_qmv_bf16_t(const QmmArgs &a, hipStream_t st) {
   constexpr int T = 64 * QMV_WAVES;
   dim3 grid((a.N + R * QMV_WAVES - 1) / (R * QMV_WAVES));
   const uint16_t *x = (const uint16_t *)a.x;
-  uint16_t *y = (uint16_t *)a.y;
+  const YOut y = yout_of(a);
   if (lds <= QMV_LDS_MAX && pieces <= 2 * T)
-    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 2, DB>), grid, dim3(T), lds, st, x, a.w, a.s, y, a.N, a.K);
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 2, DB, false, PARTS>), grid, dim3(T), lds, st, x, a.w, a.s,
+                       y, a.N, a.K);
   else if (lds <= QMV_LDS_MAX && pieces <= 4 * T)
-    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 4, DB>), grid, dim3(T), lds, st, x, a.w, a.s, y, a.N, a.K);
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 4, DB, false, PARTS>), grid, dim3(T), lds, st, x, a.w, a.s,
+                       y, a.N, a.K);
   else
-    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 0, DB>), grid, dim3(T), 0, st, x, a.w, a.s, y, a.N, a.K);
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 0, DB, false, PARTS>), grid, dim3(T), 0, st, x, a.w, a.s,
+                       y, a.N, a.K);
   return hipGetLastError();
 }
 
@@ -459,15 +468,21 @@ static hipError_t launch_qmv_bf16_t(const QmmArgs &a, hipStream_t st) {
 // rows leave too few blocks (N = 5120 at M = 1: 8.4 us against 6.8 us).
 // Single-segment shapes only (C <= 320 chunks: nvfp4 K <= 10240, mxfp8 K <= 5120);
 // longer rows use the long-row kernel.
-template <int MODE, int M>
-static hipError_t launch_qmv_bf16_m(const QmmArgs &a, hipStream_t st) {
+template <int MODE, int M, bool PARTS>
+static hipError_t launch_qmv_bf16_p(const QmmArgs &a, hipStream_t st) {
   const int C = MODE == MXFP8 ? a.K / 16 : a.K / 32;
   if (M == 1 && a.N < 16384) {
-    if (C <= 3 * 64) return launch_qmv_bf16_t<MODE, M, 1, 3, false>(a, st);
-    return launch_qmv_bf16_t<MODE, M, 1, 5, false>(a, st);
+    if (C <= 3 * 64) return launch_qmv_bf16_t<MODE, M, 1, 3, false, PARTS>(a, st);
+    return launch_qmv_bf16_t<MODE, M, 1, 5, false, PARTS>(a, st);
   }
-  if (C <= 3 * 64) return launch_qmv_bf16_t<MODE, M, 2, 3, false>(a, st);
-  return launch_qmv_bf16_t<MODE, M, 2, 5, false>(a, st);
+  if (C <= 3 * 64) return launch_qmv_bf16_t<MODE, M, 2, 3, false, PARTS>(a, st);
+  return launch_qmv_bf16_t<MODE, M, 2, 5, false, PARTS>(a, st);
+}
+
+// (the grouped instances, with the output part lookup, only for grouped calls)
+template <int MODE, int M>
+static hipError_t launch_qmv_bf16_m(const QmmArgs &a, hipStream_t st) {
+  return a.parts ? launch_qmv_bf16_p<MODE, M, true>(a, st) : launch_qmv_bf16_p<MODE, M, false>(a, st);
 }
 
 template <int MODE>
@@ -489,7 +504,7 @@ static hipError_t launch_qmv_mlp_m(const QmmArgs &a, const uint8_t *w_up, const 
   constexpr int T = 64 * QMV_WAVES;
   dim3 grid((a.N + QMV_WAVES - 1) / QMV_WAVES);
   const uint16_t *x = (const uint16_t *)a.x;
-  uint16_t *y = (uint16_t *)a.y;
+  const YOut y = yout_of(a);
 #define QMV_MLP_LAUNCH(IS, XP)                                                                                 \
   hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, 2, IS, XP, false, true>), grid, dim3(T), XP ? lds : 0, st, x, a.w, \
                      a.s, y, a.N, a.K, w_up, s_up)
@@ -543,7 +558,7 @@ template <int MODE, int M, int ISEG, int R>
 __global__ __launch_bounds__(64 * QLONG_WAVES) void qmv_long_kernel(const uint16_t *__restrict__ x,
                                                                     const uint8_t *__restrict__ w,
                                                                     const uint8_t *__restrict__ s,
-                                                                    uint16_t *__restrict__ y, int N, int K) {
+                                                                    const YOut yo, int N, int K) {
   using L = XLayout<MODE>;
   constexpr int T = 64 * QLONG_WAVES;
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
@@ -676,7 +691,7 @@ __global__ __launch_bounds__(64 * QLONG_WAVES) void qmv_long_kernel(const uint16
           out = lane == r * M + m ? v : out;
           acc[r][m] = 0.f;
         }
-      if (lane < R * M && n0 + lane / M < N) y[(int64_t)(lane % M) * N + n0 + lane / M] = f32_to_bf16_rne(out);
+      if (lane < R * M && n0 + lane / M < N) yo.y0[(int64_t)(lane % M) * N + n0 + lane / M] = f32_to_bf16_rne(out);
     }
   };
   // two units in flight: compute one while the next one's loads land
@@ -714,7 +729,7 @@ static hipError_t launch_qmv_long_t(const QmmArgs &a, hipStream_t st) {
   const int want = ((a.N + R - 1) / R + QLONG_WAVES - 1) / QLONG_WAVES, have = cus * (per_cu > 0 ? per_cu : 1);
   dim3 grid(want < have ? want : have);
   hipLaunchKernelGGL((qmv_long_kernel<MODE, M, ISEG, R>), grid, dim3(64 * QLONG_WAVES), lds, st, (const uint16_t *)a.x,
-                     a.w, a.s, (uint16_t *)a.y, a.N, a.K);
+                     a.w, a.s, yout_of(a), a.N, a.K);
   return hipGetLastError();
 }
 
@@ -769,6 +784,16 @@ hipError_t launch_qmv(const QmmArgs &a, hipStream_t st) {
   if (qmv_long_ok(a)) return a.mode == MXFP8 ? launch_qmv_long<MXFP8>(a, st) : launch_qmv_long<NVFP4>(a, st);
   if (a.mode == MXFP8) return a.x_f32 ? launch_qmv_mode<MXFP8, true>(a, st) : launch_qmv_mode<MXFP8, false>(a, st);
   return a.x_f32 ? launch_qmv_mode<NVFP4, true>(a, st) : launch_qmv_mode<NVFP4, false>(a, st);
+}
+
+// The kernels with grouped instances: the two MFMA forms at one pass and the
+// bf16 GEMV, i.e. what run_qmm picks for bf16 x, M <= 4, 16-byte aligned x and
+// W, at K = 5120 (MFMA) or single-segment rows (bf16 GEMV).
+bool qmv_parts_ok(const QmmArgs &a) {
+  if (a.x_f32 || a.M < 1 || a.M > 4 || a.N < 1 || a.K < 1) return false;
+  if ((((uintptr_t)a.x) | ((uintptr_t)a.w)) & 15) return false;
+  if (qmv_mfma_ok(a)) return qmv_mfma_parts_ok(a);
+  return qmv_fast_ok(a) && qmv_single_segment(a);
 }
 
 bool qmv_mlp_ok(const QmmArgs &a) {

@@ -172,11 +172,11 @@ constexpr size_t qf_lds_bytes(int M, int Q, int F) {
 // p Q + q (a slice past K re-reads the last slice and its sums are replaced by
 // zero), re-splits x for it and adds its partial sums to those of earlier
 // passes; the partials of every row block stay in LDS until the last pass.
-template <int MODE, int M, int Q, int NMAT, int D, int P>
+template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false>
 __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__restrict__ x,
                                                           const uint8_t *__restrict__ w,
                                                           const uint8_t *__restrict__ s, const uint8_t *__restrict__ w2,
-                                                          const uint8_t *__restrict__ s2, uint16_t *__restrict__ y,
+                                                          const uint8_t *__restrict__ s2, const YOut yo,
                                                           int N, int K, int F) {
   using G = QfGeom<MODE>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -314,7 +314,14 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
         for (int qq = 0; qq < Q; ++qq) sum[mat] += pp[16 * qq + 8 * mat];
       }
       const float out = NMAT == 2 ? silu_mul_bf16(sum[0], sum[NMAT - 1]) : sum[0];
-      if (row < r_end) y[(int64_t)m * N + row] = f32_to_bf16_rne(out);
+      if (row < r_end) {
+        // (the part lookup only in the grouped instances: it costs registers in the loop)
+        const uint16_t v = f32_to_bf16_rne(out);
+        if constexpr (PARTS)
+          *yo.at(m, row) = v;
+        else
+          yo.y0[(int64_t)m * N + row] = v;
+      }
     }
     lds_barrier();
   };
@@ -442,12 +449,12 @@ constexpr size_t q32_lds_bytes(int M, int Q, int F) { return (size_t)Q * Q32_WAV
 
 // NMAT = 2: the MLP form, a unit's 32 columns being 16 rows of W (gate) and the
 // same 16 rows of W2 (up); the flush writes silu(gate) * up (as in qmv_mfma_kernel).
-template <int M, int Q, int P, int NMAT>
+template <int M, int Q, int P, int NMAT, bool PARTS = false>
 __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__restrict__ x,
                                                             const uint8_t *__restrict__ w,
                                                             const uint8_t *__restrict__ s,
                                                             const uint8_t *__restrict__ w2,
-                                                            const uint8_t *__restrict__ s2, uint16_t *__restrict__ y,
+                                                            const uint8_t *__restrict__ s2, const YOut yo,
                                                             int N, int K, int F) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
@@ -532,7 +539,14 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
         for (int qh = 0; qh < 2 * Q; ++qh) sum[mat] += pp[32 * qh + 16 * mat];
       }
       const float out = NMAT == 2 ? silu_mul_bf16(sum[0], sum[NMAT - 1]) : sum[0];
-      if (row < r_end) y[(int64_t)m * N + row] = f32_to_bf16_rne(out);
+      if (row < r_end) {
+        // (the part lookup only in the grouped instances: it costs registers in the loop)
+        const uint16_t v = f32_to_bf16_rne(out);
+        if constexpr (PARTS)
+          *yo.at(m, row) = v;
+        else
+          yo.y0[(int64_t)m * N + row] = v;
+      }
     }
     lds_barrier();
   };
@@ -682,10 +696,10 @@ bool qmv_mfma_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up)
   return (((uintptr_t)w_up) & 15) == 0 && (((uintptr_t)s_up) & 7) == 0;
 }
 
-template <int MODE, int M, int Q, int NMAT, int D, int P>
+template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false>
 static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
                             hipStream_t st) {
-  auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D, P>;
+  auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D, P, PARTS>;
   const size_t lds = qf_lds_bytes<MODE>(M, Q, F);
   static bool attr_set = false;
   if (!attr_set) {
@@ -694,7 +708,7 @@ static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *
     attr_set = true;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), lds, st, (const uint16_t *)a.x, a.w, a.s, w2, s2,
-                     (uint16_t *)a.y, a.N, a.K, F);
+                     yout_of(a), a.N, a.K, F);
   return hipGetLastError();
 }
 
@@ -702,18 +716,19 @@ static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *
 // is then a few memory latencies long); one otherwise, which streams faster.
 // K = 17408 (three passes, no MLP form) keeps one unit in flight: x of all
 // passes is held in registers.
-template <int MODE, int M, int NMAT>
+// (grouped calls, PARTS, run one pass only: K = 5120)
+template <int MODE, int M, int NMAT, bool PARTS = false>
 static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F, int nrb,
                               hipStream_t st) {
-  if constexpr (NMAT == 1)
+  if constexpr (NMAT == 1 && !PARTS)
     if (qf_shape(a.K).P == 3) return launch_qf<MODE, M, 12, 1, 1, 3>(a, w2, s2, grid, F, st);
-  // (the MLP form at nvfp4 M = 2 would spill with two units in flight)
-  if constexpr (!(NMAT == 2 && MODE == NVFP4 && M == 2))
-    if (nrb <= 4) return launch_qf<MODE, M, 10, NMAT, 2, 1>(a, w2, s2, grid, F, st);
-  return launch_qf<MODE, M, 10, NMAT, 1, 1>(a, w2, s2, grid, F, st);
+  // (the MLP form and the grouped form at nvfp4 M = 2 would spill with two units in flight)
+  if constexpr (!((NMAT == 2 || PARTS) && MODE == NVFP4 && M == 2))
+    if (nrb <= 4) return launch_qf<MODE, M, 10, NMAT, 2, 1, PARTS>(a, w2, s2, grid, F, st);
+  return launch_qf<MODE, M, 10, NMAT, 1, 1, PARTS>(a, w2, s2, grid, F, st);
 }
 
-template <int NMAT>
+template <int NMAT, bool PARTS = false>
 static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, hipStream_t st) {
   const int cus = qf_cus();
   if (cus == 0) return hipErrorNoDevice;
@@ -723,22 +738,22 @@ static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8
   const int F = qf_flush_rows(a, nrb);
   if (qf_shape(a.K).P > 1 && F < nrb) return hipErrorInvalidValue;
   if (a.mode == NVFP4) {
-    if (a.M == 1) return launch_qf_d<NVFP4, 1, NMAT>(a, w2, s2, grid, F, nrb, st);
-    return launch_qf_d<NVFP4, 2, NMAT>(a, w2, s2, grid, F, nrb, st);
+    if (a.M == 1) return launch_qf_d<NVFP4, 1, NMAT, PARTS>(a, w2, s2, grid, F, nrb, st);
+    return launch_qf_d<NVFP4, 2, NMAT, PARTS>(a, w2, s2, grid, F, nrb, st);
   }
   switch (a.M) {
-    case 1: return launch_qf_d<MXFP8, 1, NMAT>(a, w2, s2, grid, F, nrb, st);
-    case 2: return launch_qf_d<MXFP8, 2, NMAT>(a, w2, s2, grid, F, nrb, st);
-    case 3: return launch_qf_d<MXFP8, 3, NMAT>(a, w2, s2, grid, F, nrb, st);
-    default: return launch_qf_d<MXFP8, 4, NMAT>(a, w2, s2, grid, F, nrb, st);
+    case 1: return launch_qf_d<MXFP8, 1, NMAT, PARTS>(a, w2, s2, grid, F, nrb, st);
+    case 2: return launch_qf_d<MXFP8, 2, NMAT, PARTS>(a, w2, s2, grid, F, nrb, st);
+    case 3: return launch_qf_d<MXFP8, 3, NMAT, PARTS>(a, w2, s2, grid, F, nrb, st);
+    default: return launch_qf_d<MXFP8, 4, NMAT, PARTS>(a, w2, s2, grid, F, nrb, st);
   }
 }
 
 // nvfp4 on the 32x32x64 form: 32-row blocks, one unit in flight per wave.
-template <int M, int Q, int P, int NMAT>
+template <int M, int Q, int P, int NMAT, bool PARTS = false>
 static hipError_t launch_q32(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
                              hipStream_t st) {
-  auto kern = qmv_mfma32_kernel<M, Q, P, NMAT>;
+  auto kern = qmv_mfma32_kernel<M, Q, P, NMAT, PARTS>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -746,7 +761,7 @@ static hipError_t launch_q32(const QmmArgs &a, const uint8_t *w2, const uint8_t 
     attr_set = true;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), q32_lds_bytes(M, Q, F), st, (const uint16_t *)a.x, a.w, a.s, w2,
-                     s2, (uint16_t *)a.y, a.N, a.K, F);
+                     s2, yout_of(a), a.N, a.K, F);
   return hipGetLastError();
 }
 
@@ -782,6 +797,11 @@ static hipError_t launch_q32_any(const QmmArgs &a, hipStream_t st) {
   const int F = q32_flush_rows(a, nrb);
   const bool three = qf_shape(a.K).P == 3;
   const uint8_t *w2 = a.w, *s2 = a.s;  // unused in the plain form
+  if (a.parts) {  // grouped calls: one pass (K = 5120), M = 3-4
+    if (three || a.M < 3) return hipErrorInvalidValue;
+    return a.M == 3 ? launch_q32<3, 10, 1, 1, true>(a, w2, s2, grid, F, st)
+                    : launch_q32<4, 10, 1, 1, true>(a, w2, s2, grid, F, st);
+  }
   switch (a.M) {
     case 1: return three ? launch_q32<1, 12, 3, 1>(a, w2, s2, grid, F, st) : launch_q32<1, 10, 1, 1>(a, w2, s2, grid, F, st);
     case 2: return three ? launch_q32<2, 12, 3, 1>(a, w2, s2, grid, F, st) : launch_q32<2, 10, 1, 1>(a, w2, s2, grid, F, st);
@@ -809,8 +829,12 @@ static hipError_t launch_q32_mlp(const QmmArgs &a, const uint8_t *w_up, const ui
 hipError_t launch_qmv_mfma(const QmmArgs &a, hipStream_t st) {
   if (!qmv_mfma_ok(a)) return hipErrorInvalidValue;
   if (a.mode == NVFP4 && a.M > 2) return launch_q32_any(a, st);
+  if (a.parts) return qf_shape(a.K).P == 1 ? launch_qf_any<1, true>(a, a.w, a.s, st) : hipErrorInvalidValue;
   return launch_qf_any<1>(a, a.w, a.s, st);
 }
+
+// Grouped calls on these kernels: one pass over K (K = 5120).
+bool qmv_mfma_parts_ok(const QmmArgs &a) { return qmv_mfma_ok(a) && qf_shape(a.K).P == 1; }
 
 hipError_t launch_qmv_mfma_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st) {
   if (!qmv_mfma_mlp_ok(a, w_up, s_up)) return hipErrorInvalidValue;

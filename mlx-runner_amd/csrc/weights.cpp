@@ -412,7 +412,128 @@ int load_weights(const std::string &dir, hipStream_t st, WeightMap **out) {
     if (!seen) shards.push_back(kv.second.str);
   }
   std::unique_ptr<WeightMap> m(new WeightMap());
-  std::vector<TensorInfo> all;
+  // 1) every shard's header: the tensors to load, with their file and data offset
+  struct Item {
+    size_t shard;          // index into fds
+    const TensorInfo *t;
+    std::string kept;      // name after sanitize_name
+    size_t bytes;
+    void *dev = nullptr;   // destination in HBM
+  };
+  std::vector<int> fds;
+  std::vector<uint64_t> data_starts;
+  std::vector<std::vector<TensorInfo>> shard_infos(shards.size());
+  auto close_all = [&]() {
+    for (int fd : fds) ::close(fd);
+    fds.clear();
+  };
+  std::vector<Item> items;
+  std::unordered_map<std::string, size_t> index;  // kept name -> items index
+  for (size_t si = 0; si < shards.size(); ++si) {
+    const std::string path = dir + "/" + shards[si];
+    int fd = ::open(path.c_str(), O_RDONLY);
+    if (fd < 0) {
+      close_all();
+      fail("[qmm_weights_load] cannot open %s", path.c_str());
+      return QMM_WE_IO;
+    }
+    fds.push_back(fd);
+    uint64_t data_start = 0;
+    rc = read_shard_header(fd, shard_infos[si], &data_start);
+    if (rc) {
+      close_all();
+      return rc;
+    }
+    data_starts.push_back(data_start);
+    for (auto &t : shard_infos[si]) {
+      std::string kept;
+      if (!sanitize_name(t.name, kept)) continue;
+      if (index.count(kept)) {
+        close_all();
+        return QMM_WE_DUPLICATE_TENSOR;
+      }
+      long long numel = 1;
+      for (long long d : t.shape) numel *= d;
+      const size_t bytes = (size_t)numel * dsize(t.dtype);
+      if (t.off0 < 0 || t.off1 < t.off0 || (size_t)(t.off1 - t.off0) != bytes || t.shape.size() > QMM_MAX_DIM) {
+        close_all();
+        return QMM_WE_BAD_HEADER;
+      }
+      index.emplace(kept, items.size());
+      items.push_back(Item{si, &t, kept, bytes});
+    }
+  }
+
+  // 2) placement.  The packed weights (and, separately, the scales) of projections
+  //    that share their input are placed back to back in one allocation, so one
+  //    grouped call runs them as one matrix: each member's rows follow the previous
+  //    member's.  Everything else gets its own allocation.
+  static const std::vector<std::vector<const char *>> kGroups = {
+      {"linear_attn.in_proj_qkv", "linear_attn.in_proj_z", "linear_attn.in_proj_b", "linear_attn.in_proj_a"},
+      {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"},
+      {"mlp.gate_proj", "mlp.up_proj"},
+  };
+  auto alloc = [&](void **dev, size_t bytes, const std::string &what) -> int {
+    *dev = nullptr;
+    if (!bytes) return 0;
+    hipError_t e = hipMalloc(dev, bytes);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      fail("[qmm_weights_load] Unable to allocate %zu bytes for %s (out of memory)", bytes, what.c_str());
+      return QMM_WE_IO;
+    }
+    m->buffers.push_back(*dev);
+    return 0;
+  };
+  for (const char *kind : {".weight", ".scales"}) {
+    const DType want = std::strcmp(kind, ".weight") == 0 ? DType::U32 : DType::U8;
+    for (const auto &g : kGroups) {
+      // the first member's tensors name the layers that have this group
+      const std::string first = std::string(g[0]) + kind;
+      for (auto &it : items) {
+        if (!ends_with(it.kept, first.c_str()) || it.kept.size() == first.size() ||
+            it.kept[it.kept.size() - first.size() - 1] != '.')
+          continue;
+        const std::string prefix = it.kept.substr(0, it.kept.size() - first.size());
+        std::vector<Item *> mem;
+        for (const char *name : g) {
+          auto f = index.find(prefix + name + kind);
+          if (f == index.end()) break;
+          Item *x = &items[f->second];
+          if (x->dev || x->t->dtype != want || x->t->shape.size() != 2 || x->t->shape[1] != it.t->shape[1]) break;
+          mem.push_back(x);
+        }
+        if (mem.size() != g.size()) continue;
+        // every member starts 256-byte aligned, as its own allocation would
+        size_t total = 0;
+        bool aligned = true;
+        for (size_t j = 0; j < mem.size(); ++j) {
+          aligned = aligned && (j + 1 == mem.size() || mem[j]->bytes % 256 == 0);
+          total += mem[j]->bytes;
+        }
+        if (!aligned || !total) continue;
+        void *base = nullptr;
+        if (alloc(&base, total, prefix + g[0] + kind)) {
+          close_all();
+          return QMM_WE_IO;
+        }
+        size_t off = 0;
+        for (Item *x : mem) {
+          x->dev = (char *)base + off;
+          off += x->bytes;
+        }
+      }
+    }
+  }
+  for (auto &it : items) {
+    if (it.dev || !it.bytes) continue;
+    if (alloc(&it.dev, it.bytes, it.t->name)) {
+      close_all();
+      return QMM_WE_IO;
+    }
+  }
+
+  // 3) raw copies: file -> pinned stage -> HBM, reads of at most 1 GiB
   const size_t kStage = 64ull << 20, kMaxRead = 1ull << 30;
   void *stage[2] = {nullptr, nullptr};
   hipEvent_t done[2];
@@ -420,6 +541,7 @@ int load_weights(const std::string &dir, hipStream_t st, WeightMap **out) {
     if (hipHostMalloc(&stage[i], kStage, hipHostMallocDefault) != hipSuccess) {
       (void)hipGetLastError();
       for (int j = 0; j < i; ++j) (void)hipHostFree(stage[j]);
+      close_all();
       fail("[qmm_weights_load] Unable to allocate pinned staging buffer (out of memory)");
       return QMM_WE_IO;
     }
@@ -433,85 +555,42 @@ int load_weights(const std::string &dir, hipStream_t st, WeightMap **out) {
       (void)hipHostFree(stage[i]);
       (void)hipEventDestroy(done[i]);
     }
+    close_all();
   };
-  for (auto &shard : shards) {
-    const std::string path = dir + "/" + shard;
-    int fd = ::open(path.c_str(), O_RDONLY);
-    if (fd < 0) {
-      cleanup();
-      fail("[qmm_weights_load] cannot open %s", path.c_str());
-      return QMM_WE_IO;
-    }
-    std::vector<TensorInfo> infos;
-    uint64_t data_start = 0;
-    rc = read_shard_header(fd, infos, &data_start);
-    if (rc) {
-      ::close(fd);
-      cleanup();
-      return rc;
-    }
-    for (auto &t : infos) {
-      std::string kept;
-      if (!sanitize_name(t.name, kept)) continue;
-      if (m->map.count(kept)) {
-        ::close(fd);
+  for (auto &it : items) {
+    const int fd = fds[it.shard];
+    const uint64_t data_start = data_starts[it.shard];
+    size_t done_bytes = 0;
+    while (done_bytes < it.bytes) {
+      size_t n = it.bytes - done_bytes;
+      if (n > kStage) n = kStage;
+      if (n > kMaxRead) n = kMaxRead;
+      if (used[cur]) (void)hipEventSynchronize(done[cur]);
+      if (!pread_all(fd, stage[cur], n, (off_t)(data_start + it.t->off0 + done_bytes))) {
         cleanup();
-        return QMM_WE_DUPLICATE_TENSOR;
+        fail("[qmm_weights_load] short read in %s", (dir + "/" + shards[it.shard]).c_str());
+        return QMM_WE_IO;
       }
-      long long numel = 1;
-      for (long long d : t.shape) numel *= d;
-      const size_t bytes = (size_t)numel * dsize(t.dtype);
-      if (t.off0 < 0 || t.off1 < t.off0 || (size_t)(t.off1 - t.off0) != bytes || t.shape.size() > QMM_MAX_DIM) {
-        ::close(fd);
+      hipError_t e = hipMemcpyAsync((char *)it.dev + done_bytes, stage[cur], n, hipMemcpyHostToDevice, st);
+      if (e == hipSuccess) e = hipEventRecord(done[cur], st);
+      if (e != hipSuccess) {
         cleanup();
-        return QMM_WE_BAD_HEADER;
+        fail_hip(e, "qmm_weights_load");
+        return QMM_WE_IO;
       }
-      void *dev = nullptr;
-      if (bytes) {
-        hipError_t e = hipMalloc(&dev, bytes);
-        if (e != hipSuccess) {
-          (void)hipGetLastError();
-          ::close(fd);
-          cleanup();
-          fail("[qmm_weights_load] Unable to allocate %zu bytes for %s (out of memory)", bytes, t.name.c_str());
-          return QMM_WE_IO;
-        }
-        m->buffers.push_back(dev);
-      }
-      // raw copy: file -> pinned stage -> HBM, reads of at most 1 GiB
-      size_t done_bytes = 0;
-      while (done_bytes < bytes) {
-        size_t n = bytes - done_bytes;
-        if (n > kStage) n = kStage;
-        if (n > kMaxRead) n = kMaxRead;
-        if (used[cur]) (void)hipEventSynchronize(done[cur]);
-        if (!pread_all(fd, stage[cur], n, (off_t)(data_start + t.off0 + done_bytes))) {
-          ::close(fd);
-          cleanup();
-          fail("[qmm_weights_load] short read in %s", path.c_str());
-          return QMM_WE_IO;
-        }
-        hipError_t e = hipMemcpyAsync((char *)dev + done_bytes, stage[cur], n, hipMemcpyHostToDevice, st);
-        if (e == hipSuccess) e = hipEventRecord(done[cur], st);
-        if (e != hipSuccess) {
-          ::close(fd);
-          cleanup();
-          fail_hip(e, "qmm_weights_load");
-          return QMM_WE_IO;
-        }
-        used[cur] = true;
-        cur ^= 1;
-        done_bytes += n;
-      }
-      std::vector<int> shp(t.shape.begin(), t.shape.end());
-      Arr *a = new_arr(shp.data(), (int)shp.size(), to_qmm(t.dtype));
-      a->data = dev;
-      a->owned = false;  // the map owns the buffer
-      m->map.emplace(kept, a);
+      used[cur] = true;
+      cur ^= 1;
+      done_bytes += n;
     }
-    ::close(fd);
-    for (auto &t : infos) all.push_back(std::move(t));
+    std::vector<int> shp(it.t->shape.begin(), it.t->shape.end());
+    Arr *a = new_arr(shp.data(), (int)shp.size(), to_qmm(it.t->dtype));
+    a->data = it.dev;
+    a->owned = false;  // the map owns the buffer
+    m->map.emplace(it.kept, a);
   }
+  std::vector<TensorInfo> all;
+  for (auto &v : shard_infos)
+    for (auto &t : v) all.push_back(t);
   cleanup();
   rc = infer_quant_spec(all, &m->quant);
   if (rc) return rc;
@@ -597,6 +676,38 @@ int qmm_named_linear_q(qmm_array *res, qmm_weight_map m, qmm_array x, const char
   return qmm_quantized_matmul(res, x, w, sc, qmm_array{nullptr}, true,
                               qmm_optional_int{(int)wm->quant.group_size, true},
                               qmm_optional_int{(int)wm->quant.bits, true}, mode, s);
+}
+
+// Several projections of one x by checkpoint names (the GDN layer's in_proj_qkv /
+// z / b / a, src/model.zig:1066-1074; attention's q / k / v, :929-944): one grouped
+// call (qmm_quantized_matmul_group) when every weight is packed with scales,
+// otherwise named_linear_q per name.  res[i] is the result for names[i].
+int qmm_named_linear_q_group(qmm_array *res, size_t n, qmm_weight_map m, qmm_array x, const char *const *names,
+                             qmm_stream s) {
+  WeightMap *wm = (WeightMap *)m.ctx;
+  if (!wm || !names || !res) return finish(fail("[named_linear_q_group] null weight map, names or results"));
+  if (n < 1 || n > 4) return finish(fail("[named_linear_q_group] takes 1 to 4 names, got %zu", n));
+  qmm_array w[4], sc[4];
+  bool packed = wm->quant.mode != QMM_QUANT_NONE;
+  for (size_t i = 0; i < n; ++i) {
+    if (!names[i]) return finish(fail("[named_linear_q_group] null name"));
+    w[i] = qmm_weights_get(m, names[i]);
+    if (!w[i].ctx) return QMM_WE_MISSING_WEIGHT;
+    const std::string nm(names[i]);
+    sc[i] = ends_with(nm, ".weight") ? qmm_weights_get(m, (nm.substr(0, nm.size() - 7) + ".scales").c_str())
+                                     : qmm_array{nullptr};
+    packed = packed && sc[i].ctx && ((Arr *)w[i].ctx)->dtype == QMM_UINT32;
+  }
+  if (packed) {
+    const char *mode = wm->quant.mode == QMM_QUANT_MXFP8 ? "mxfp8" : "nvfp4";
+    return qmm_quantized_matmul_group(res, n, x, w, sc, qmm_optional_int{(int)wm->quant.group_size, true},
+                                      qmm_optional_int{(int)wm->quant.bits, true}, mode, s);
+  }
+  for (size_t i = 0; i < n; ++i) {
+    const int rc = qmm_named_linear_q(&res[i], m, x, names[i], s);
+    if (rc) return rc;
+  }
+  return 0;
 }
 
 // mlpForwardQ (src/model.zig:905-915): down(silu(gate(x)) * up(x)), the projections

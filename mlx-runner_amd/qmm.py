@@ -111,6 +111,7 @@ _SIGS = {
     "qmm_fault_arm": (None, [c_uint64]),
     "qmm_fault_did_fire": (c_bool, []),
     "qmm_op_count": (c_uint64, []),
+    "qmm_group_launch_count": (c_uint64, []),
     "qmm_infer_quant_spec_json": (c_int, [c_char_p, c_size_t, POINTER(qmm_quant_spec), POINTER(c_size_t)]),
     "qmm_parse_header_json": (c_int, [c_char_p, c_size_t, POINTER(c_size_t)]),
     "qmm_sanitize_name": (c_int, [c_char_p, c_char_p, c_size_t]),
@@ -128,6 +129,11 @@ _SIGS = {
                                      qmm_optional_int, qmm_optional_int, c_char_p, qmm_stream]),
     "qmm_mlp_forward_q": (c_int, [POINTER(qmm_array), qmm_weight_map, qmm_array, c_char_p, c_char_p, c_char_p,
                                   qmm_stream]),
+    "qmm_quantized_matmul_group": (c_int, [POINTER(qmm_array), c_size_t, qmm_array, POINTER(qmm_array),
+                                           POINTER(qmm_array), qmm_optional_int, qmm_optional_int, c_char_p,
+                                           qmm_stream]),
+    "qmm_named_linear_q_group": (c_int, [POINTER(qmm_array), c_size_t, qmm_weight_map, qmm_array,
+                                         POINTER(c_char_p), qmm_stream]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
@@ -341,6 +347,24 @@ def mlp_gate_up_silu(x: Array, w_gate: Array, s_gate: Array, w_up: Array, s_up: 
     return res
 
 
+def quantized_matmul_group(x: Array, ws, scales, mode: str, *, group_size=None, bits=None, outs=None,
+                           stream: Stream | None = None) -> list:
+    """[x @ deq(w_i).T for each (w_i, scales_i)]: projections of one x (src/model.zig:1066-1074,
+    :929-944), one launch when the matrices lie back to back in memory."""
+    n = len(ws)
+    assert len(scales) == n
+    res = list(outs) if outs is not None else [Array() for _ in range(n)]
+    hs = (qmm_array * n)(*[r.h for r in res])
+    wv = (qmm_array * n)(*[w.h for w in ws])
+    sv = (qmm_array * n)(*[sc.h for sc in scales])
+    s = _stream(stream)
+    rc = lib.qmm_quantized_matmul_group(hs, n, x.h, wv, sv, opt_int(group_size), opt_int(bits), mode.encode(), s.h)
+    for r, h in zip(res, hs):
+        r.h = h
+    check(rc, "quantized_matmul_group")
+    return res
+
+
 def infer_quant_spec_json(header: str):
     b = header.encode()
     spec = qmm_quant_spec()
@@ -395,6 +419,20 @@ class WeightMap:
         rc = lib.qmm_named_linear_q(byref(res.h), self.h, x.h, name.encode(), s.h)
         if rc:
             raise QmmError(f"named_linear_q: {WE.get(rc, rc)}: {take_error()}")
+        return res
+
+    def named_linear_q_group(self, x: Array, names, stream: Stream | None = None) -> list:
+        """Projections of one x by name, one grouped call when all are packed with scales."""
+        n = len(names)
+        res = [Array() for _ in range(n)]
+        hs = (qmm_array * n)(*[r.h for r in res])
+        nm = (c_char_p * n)(*[x_.encode() for x_ in names])
+        s = _stream(stream)
+        rc = lib.qmm_named_linear_q_group(hs, n, self.h, x.h, nm, s.h)
+        for r, h in zip(res, hs):
+            r.h = h
+        if rc:
+            raise QmmError(f"named_linear_q_group: {WE.get(rc, rc)}: {take_error()}")
         return res
 
     def mlp_forward_q(self, x: Array, gate: str, down: str, up: str, stream: Stream | None = None) -> Array:
