@@ -617,16 +617,21 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
 
 }  // namespace
 
-// Waves per workgroup (Q) and passes (P) for K: the decode shapes served are
-// K = 5120 (10 slices of 512: Q = 10, P = 1) and K = 17408 (34 slices: Q = 12,
-// P = 3, two slices of the last pass past K).
+// Waves per workgroup (Q) and passes (P) for K, the model's row lengths:
+// K = 5120 (10 slices of 512: Q = 10, P = 1), 6144 (o_proj / out_proj: 12
+// slices, Q = 12, P = 1), 10240 (mtp.fc: 20 slices, Q = 10, P = 2) and 17408
+// (down: 34 slices, Q = 12, P = 3, two slices of the last pass past K).
 struct QfShape {
   int Q, P;
 };
 static QfShape qf_shape(int K) {
-  if (K == 5120) return {10, 1};
-  if (K == 17408) return {12, 3};
-  return {0, 0};
+  switch (K) {
+    case 5120: return {10, 1};
+    case 6144: return {12, 1};
+    case 10240: return {10, 2};
+    case 17408: return {12, 3};
+    default: return {0, 0};
+  }
 }
 
 static int qf_cus() {
@@ -691,7 +696,7 @@ static bool q32_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_u
 // The fused MLP form: the 16x16x128 kernel (nvfp4 M <= 2, mxfp8 M <= 4) and the
 // 32x32x64 kernel at one pass (nvfp4 M = 3-4, K = 5120).
 bool qmv_mfma_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up) {
-  if (!qmv_mfma_ok(a)) return false;
+  if (!qmv_mfma_ok(a) || a.K != 5120) return false;
   if (a.mode == NVFP4 && a.M > 2) return q32_mlp_ok(a, w_up, s_up);
   return (((uintptr_t)w_up) & 15) == 0 && (((uintptr_t)s_up) & 7) == 0;
 }
@@ -716,12 +721,16 @@ static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *
 // is then a few memory latencies long); one otherwise, which streams faster.
 // K = 17408 (three passes, no MLP form) keeps one unit in flight: x of all
 // passes is held in registers.
-// (grouped calls, PARTS, run one pass only: K = 5120)
+// (grouped calls, PARTS, and the MLP form run K = 5120 only)
 template <int MODE, int M, int NMAT, bool PARTS = false>
 static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F, int nrb,
                               hipStream_t st) {
-  if constexpr (NMAT == 1 && !PARTS)
-    if (qf_shape(a.K).P == 3) return launch_qf<MODE, M, 12, 1, 1, 3>(a, w2, s2, grid, F, st);
+  if constexpr (NMAT == 1 && !PARTS) {
+    const QfShape g = qf_shape(a.K);
+    if (g.P == 3) return launch_qf<MODE, M, 12, 1, 1, 3>(a, w2, s2, grid, F, st);
+    if (g.P == 2) return launch_qf<MODE, M, 10, 1, 1, 2>(a, w2, s2, grid, F, st);
+    if (g.Q == 12) return launch_qf<MODE, M, 12, 1, 1, 1>(a, w2, s2, grid, F, st);
+  }
   // (the MLP form and the grouped form at nvfp4 M = 2 would spill with two units in flight)
   if constexpr (!((NMAT == 2 || PARTS) && MODE == NVFP4 && M == 2))
     if (nrb <= 4) return launch_qf<MODE, M, 10, NMAT, 2, 1, PARTS>(a, w2, s2, grid, F, st);
@@ -788,6 +797,15 @@ static bool q32_ok(const QmmArgs &a) {
   return ((((uintptr_t)a.x) | ((uintptr_t)a.w) | ((uintptr_t)a.s)) & 15) == 0;
 }
 
+// the plain 32-row form for K's (Q, P)
+template <int M>
+static hipError_t launch_q32_k(const QmmArgs &a, QfShape g, int grid, int F, hipStream_t st) {
+  if (g.P == 3) return launch_q32<M, 12, 3, 1>(a, a.w, a.s, grid, F, st);
+  if (g.P == 2) return launch_q32<M, 10, 2, 1>(a, a.w, a.s, grid, F, st);
+  if (g.Q == 12) return launch_q32<M, 12, 1, 1>(a, a.w, a.s, grid, F, st);
+  return launch_q32<M, 10, 1, 1>(a, a.w, a.s, grid, F, st);
+}
+
 static hipError_t launch_q32_any(const QmmArgs &a, hipStream_t st) {
   if (!q32_ok(a)) return hipErrorInvalidValue;
   const int cus = qf_cus();
@@ -795,18 +813,18 @@ static hipError_t launch_q32_any(const QmmArgs &a, hipStream_t st) {
   const int grid = rbs < cus ? rbs : cus;
   const int nrb = q32_nrb(a, cus);
   const int F = q32_flush_rows(a, nrb);
-  const bool three = qf_shape(a.K).P == 3;
+  const QfShape g = qf_shape(a.K);
   const uint8_t *w2 = a.w, *s2 = a.s;  // unused in the plain form
-  if (a.parts) {  // grouped calls: one pass (K = 5120), M = 3-4
-    if (three || a.M < 3) return hipErrorInvalidValue;
+  if (a.parts) {  // grouped calls: K = 5120, M = 3-4
+    if (g.Q != 10 || g.P != 1 || a.M < 3) return hipErrorInvalidValue;
     return a.M == 3 ? launch_q32<3, 10, 1, 1, true>(a, w2, s2, grid, F, st)
                     : launch_q32<4, 10, 1, 1, true>(a, w2, s2, grid, F, st);
   }
   switch (a.M) {
-    case 1: return three ? launch_q32<1, 12, 3, 1>(a, w2, s2, grid, F, st) : launch_q32<1, 10, 1, 1>(a, w2, s2, grid, F, st);
-    case 2: return three ? launch_q32<2, 12, 3, 1>(a, w2, s2, grid, F, st) : launch_q32<2, 10, 1, 1>(a, w2, s2, grid, F, st);
-    case 3: return three ? launch_q32<3, 12, 3, 1>(a, w2, s2, grid, F, st) : launch_q32<3, 10, 1, 1>(a, w2, s2, grid, F, st);
-    default: return three ? launch_q32<4, 12, 3, 1>(a, w2, s2, grid, F, st) : launch_q32<4, 10, 1, 1>(a, w2, s2, grid, F, st);
+    case 1: return launch_q32_k<1>(a, g, grid, F, st);
+    case 2: return launch_q32_k<2>(a, g, grid, F, st);
+    case 3: return launch_q32_k<3>(a, g, grid, F, st);
+    default: return launch_q32_k<4>(a, g, grid, F, st);
   }
 }
 
@@ -829,12 +847,12 @@ static hipError_t launch_q32_mlp(const QmmArgs &a, const uint8_t *w_up, const ui
 hipError_t launch_qmv_mfma(const QmmArgs &a, hipStream_t st) {
   if (!qmv_mfma_ok(a)) return hipErrorInvalidValue;
   if (a.mode == NVFP4 && a.M > 2) return launch_q32_any(a, st);
-  if (a.parts) return qf_shape(a.K).P == 1 ? launch_qf_any<1, true>(a, a.w, a.s, st) : hipErrorInvalidValue;
+  if (a.parts) return a.K == 5120 ? launch_qf_any<1, true>(a, a.w, a.s, st) : hipErrorInvalidValue;
   return launch_qf_any<1>(a, a.w, a.s, st);
 }
 
-// Grouped calls on these kernels: one pass over K (K = 5120).
-bool qmv_mfma_parts_ok(const QmmArgs &a) { return qmv_mfma_ok(a) && qf_shape(a.K).P == 1; }
+// Grouped calls on these kernels: K = 5120.
+bool qmv_mfma_parts_ok(const QmmArgs &a) { return qmv_mfma_ok(a) && a.K == 5120; }
 
 hipError_t launch_qmv_mfma_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st) {
   if (!qmv_mfma_mlp_ok(a, w_up, s_up)) return hipErrorInvalidValue;

@@ -409,6 +409,30 @@ def test_decode_mfma_down_shapes_match_oracle(mode, M, N, xkind):
     assert np.array_equal(run_qmm(mode, xb, wq, s), y)
 
 
+# The other row lengths of the model on the MFMA kernels: K = 6144 (o_proj /
+# out_proj: 12 waves, one pass) and K = 10240 (mtp.fc: 10 waves, two passes;
+# nvfp4 M = 1 takes it too).  Edge groups in the first slice of every pass and in
+# the last slice.
+@pytest.mark.parametrize("K", [6144, 10240])
+@pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 5120), ("nvfp4", 2, 4099), ("nvfp4", 3, 5120),
+                                      ("nvfp4", 4, 4099), ("mxfp8", 2, 5120), ("mxfp8", 3, 4101),
+                                      ("mxfp8", 4, 8192)])
+@pytest.mark.parametrize("xkind", ["normal", "edge"])
+def test_decode_mfma_other_k_match_oracle(K, mode, M, N, xkind):
+    rng = np.random.default_rng(N * 10 + M + K)
+    wq, s = rand_packed(rng, mode, N, K)
+    xb = make_x(rng, M, K, xkind)
+    if xkind == "edge":
+        for off in (5120, K - 512):
+            xb[:, off:off + 128] = xb[:, 0:128]
+    y = run_qmm(mode, xb, wq, s)
+    cols = np.unique(np.concatenate([np.arange(0, N, 11), np.arange(N - 40, N), np.arange(40)]))
+    ref = O.qmm(mode, xb, wq, s, cols=cols)
+    ok, fro, worst = O.check_tolerance(f32(y[:, cols]), f32(ref), **TOL)
+    assert ok, (fro, worst)
+    assert np.array_equal(run_qmm(mode, xb, wq, s), y)
+
+
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 2, 4099), ("nvfp4", 3, 4099),
                                       ("nvfp4", 4, 16400), ("mxfp8", 3, 4101), ("mxfp8", 4, 70001)])
 def test_mlp_gate_up_silu_mfma_shapes(mode, M, N):
