@@ -63,8 +63,11 @@ __device__ __forceinline__ void ld8(const void *p, int64_t i, float (&o)[8]) {
 __device__ __forceinline__ void gdn_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // IN_F32: q, k, v are float32 (else bfloat16).  Y_F32: y is float32 (else bfloat16, RNE).
-// beta is float32 or bfloat16 (beta_f32); g and the state are float32.
-template <bool IN_F32, bool Y_F32>
+// beta is float32 or bfloat16 (beta_f32); g and the state are float32.  ONE: T fits one
+// staged block (decode), so no next block is loaded: the reload the loop issues after its
+// last block would cost the call a memory round trip (a separate instance, so that the
+// long-T loop keeps its code).
+template <bool IN_F32, bool Y_F32, bool ONE>
 __global__ __launch_bounds__(256) void gdn_kernel(const void *__restrict__ q, const void *__restrict__ k,
                                                   const void *__restrict__ v, const float *__restrict__ g,
                                                   const void *__restrict__ beta, int beta_f32,
@@ -128,10 +131,10 @@ __global__ __launch_bounds__(256) void gdn_kernel(const void *__restrict__ q, co
   stage_load(0);
   stage_store(0);
   gdn_lds_barrier();
-  const int nblk = (T + GDN_TB - 1) / GDN_TB;
+  const int nblk = ONE ? 1 : (T + GDN_TB - 1) / GDN_TB;
   for (int blk = 0; blk < nblk; ++blk) {
     const int buf = blk & 1, t0 = blk * GDN_TB;
-    stage_load(t0 + GDN_TB < T ? t0 + GDN_TB : t0);  // next block in flight (the last block reloads itself)
+    if constexpr (!ONE) stage_load(t0 + GDN_TB < T ? t0 + GDN_TB : t0);  // next block in flight (the last block reloads itself)
     const int steps = T - t0 < GDN_TB ? T - t0 : GDN_TB;
     for (int i = 0; i < steps; ++i) {
       float qv[8], kv8[8];
@@ -169,8 +172,10 @@ __global__ __launch_bounds__(256) void gdn_kernel(const void *__restrict__ q, co
           ((uint16_t *)y)[yi] = f32_to_bf16_rne(yvv);
       }
     }
-    stage_store(buf ^ 1);
-    gdn_lds_barrier();
+    if constexpr (!ONE) {
+      stage_store(buf ^ 1);
+      gdn_lds_barrier();
+    }
   }
   if (live) {
     *(float4 *)(st_out + so) = make_float4(s[0], s[1], s[2], s[3]);
@@ -180,27 +185,27 @@ __global__ __launch_bounds__(256) void gdn_kernel(const void *__restrict__ q, co
 
 }  // namespace
 
+template <bool IN, bool YF>
+static void launch_gdn_t(const GdnArgs &a, unsigned grid, hipStream_t st) {
+  if (a.T <= GDN_TB)
+    hipLaunchKernelGGL((gdn_kernel<IN, YF, true>), dim3(grid), dim3(256), 0, st, a.q, a.k, a.v, a.g, a.beta,
+                       (int)a.beta_f32, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv);
+  else
+    hipLaunchKernelGGL((gdn_kernel<IN, YF, false>), dim3(grid), dim3(256), 0, st, a.q, a.k, a.v, a.g, a.beta,
+                       (int)a.beta_f32, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv);
+}
+
 hipError_t launch_gdn(const GdnArgs &a, hipStream_t st) {
   if (a.Dk != GDN_DK || a.Dv <= 0 || a.Dv % 8 != 0 || a.Hk <= 0 || a.Hv % a.Hk != 0 || a.T <= 0 || a.B <= 0)
     return hipErrorInvalidValue;
   const int groups = (a.Dv + 15) / 16;
   const int64_t grid = (int64_t)a.B * a.Hv * groups;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
-#define GDN_LAUNCH(IN, YF)                                                                                          \
-  hipLaunchKernelGGL((gdn_kernel<IN, YF>), dim3((unsigned)grid), dim3(256), 0, st, a.q, a.k, a.v, a.g, a.beta,     \
-                     (int)a.beta_f32, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv)
-  if (a.in_f32) {
-    if (a.y_f32)
-      GDN_LAUNCH(true, true);
-    else
-      GDN_LAUNCH(true, false);
-  } else {
-    if (a.y_f32)
-      GDN_LAUNCH(false, true);
-    else
-      GDN_LAUNCH(false, false);
-  }
-#undef GDN_LAUNCH
+  const unsigned g = (unsigned)grid;
+  if (a.in_f32)
+    a.y_f32 ? launch_gdn_t<true, true>(a, g, st) : launch_gdn_t<true, false>(a, g, st);
+  else
+    a.y_f32 ? launch_gdn_t<false, true>(a, g, st) : launch_gdn_t<false, false>(a, g, st);
   return hipGetLastError();
 }
 
