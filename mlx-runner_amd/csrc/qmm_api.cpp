@@ -689,7 +689,15 @@ int qmm_gdn_recurrence(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_arra
   a.q = qa->data, a.k = ka->data, a.v = va->data, a.beta = ba->data;
   a.g = (const float *)ga->data, a.state_in = (const float *)sa->data;
   a.state_out = (float *)so->data, a.y = ya->data;
-  hipError_t e = launch_gdn(a, st);
+  hipError_t e;
+  if (gdn_chunked_ok(a)) {  // long T: the chunked form, its per-chunk matrices in a workspace
+    void *ws = nullptr;
+    if (alloc_device(&ws, gdn_chunked_workspace(a), st)) return finish(1);
+    e = launch_gdn_chunked(a, ws, st);
+    (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
+  } else {
+    e = launch_gdn(a, st);
+  }
   if (e != hipSuccess) return finish(fail_hip(e, op));
   return finish(0);
 }

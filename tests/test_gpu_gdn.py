@@ -163,3 +163,60 @@ def test_argument_checks():
     for b in bad:
         with pytest.raises(Q.QmmError):
             Q.gdn_recurrence(**{**ok, **b})
+
+
+# The chunked form (T >= 128): chunks of 64 steps on the f32 MFMA, the last chunk
+# padded with neutral steps; the same bar against the f64 oracle.
+@pytest.mark.parametrize("T", [128, 200, 1000])
+def test_chunked_model_shapes(T):
+    rng = np.random.default_rng(1000 + T)
+    q, k, v, g, beta, st = model_inputs(rng, 1, T, 16, 48, 128)
+    y, S, used = run(q, k, v, g, beta, st)
+    check(y, S, used)
+
+
+@pytest.mark.parametrize("dtypes", ["f32", "f32-beta-bf16-y-f32"])
+def test_chunked_dtypes_and_batches(dtypes):
+    rng = np.random.default_rng(77)
+    q, k, v, g, beta, st = model_inputs(rng, 2, 150, 2, 6, 32)
+    kw = {"f32": dict(in_dtype=Q.FLOAT32, beta_dtype=Q.FLOAT32),
+          "f32-beta-bf16-y-f32": dict(in_dtype=Q.FLOAT32, beta_dtype=Q.BFLOAT16, y_dtype=Q.FLOAT32)}[dtypes]
+    y, S, used = run(q, k, v, g, beta, st, **kw)
+    check(y, S, used, y_bf16=kw.get("y_dtype", Q.BFLOAT16) == Q.BFLOAT16)
+
+
+def test_chunked_extreme_decays_and_gates():
+    """Decays of exactly 1 and 0 (the state wiped mid-chunk) and tiny ones, gates of 0 and 1."""
+    rng = np.random.default_rng(78)
+    T = 300
+    q, k, v, g, beta, st = model_inputs(rng, 1, T, 4, 8, 128)
+    g[:, 10:20] = 1.0
+    g[:, 70] = 0.0
+    g[:, 100:110] = 1e-3
+    g[:, 200] = 0.0
+    beta[:, 30:40] = 0.0
+    beta[:, 40:50] = 1.0
+    y, S, used = run(q, k, v, g, beta, st)
+    check(y, S, used)
+
+
+def test_chunked_state_in_place():
+    rng = np.random.default_rng(79)
+    q, k, v, g, beta, st = model_inputs(rng, 1, 200, 16, 48, 128)
+    A = Q.Array.from_numpy
+    args = (A(bf16(q), Q.BFLOAT16), A(bf16(k), Q.BFLOAT16), A(bf16(v), Q.BFLOAT16), A(g.astype(np.float32), Q.FLOAT32),
+            A(bf16(beta), Q.BFLOAT16))
+    s_a = A(st.astype(np.float32), Q.FLOAT32)
+    y1, S1 = Q.gdn_recurrence(*args, A(st.astype(np.float32), Q.FLOAT32))
+    y2, S2 = Q.gdn_recurrence(*args, s_a, state_out=s_a)
+    assert S2.h.ctx == s_a.h.ctx
+    assert np.array_equal(y1.numpy(), y2.numpy())
+    assert np.array_equal(S1.numpy(), s_a.numpy())
+
+
+def test_long_T_rows_not_multiple_of_16_step_kernel():
+    """Dv = 24 (not a multiple of the chunked form's 16 rows): the step-by-step kernel."""
+    rng = np.random.default_rng(80)
+    q, k, v, g, beta, st = model_inputs(rng, 1, 160, 2, 4, 24)
+    y, S, used = run(q, k, v, g, beta, st)
+    check(y, S, used)
