@@ -36,8 +36,7 @@ constexpr int GR = 16;    // state rows per scan workgroup
 constexpr int KP = GDK + 4;  // LDS row pitch of [.][GDK] arrays (floats)
 constexpr int TP = GC + 4;   // LDS row pitch of [.][GC] arrays (16-byte aligned rows for float4 runs)
 
-// workspace per (b, hv, chunk), in floats; of Ap and M only the 16 x 16 blocks on and
-// below the diagonal are written (and read)
+// workspace per (b, hv, chunk), in floats (Ap and M in full, zero above the diagonal)
 constexpr int WS_AP = 0;
 constexpr int WS_M = WS_AP + GC * GC;
 constexpr int WS_GAM = WS_M + GC * GC;
@@ -243,10 +242,12 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(const void *__restrict__ q
     }
     __syncthreads();
   }
-  // Ap = A diag(beta), blocks on and below the diagonal
+  // Ap = A diag(beta); the blocks of Ap and M above the diagonal as zero
   for (int e = tid; e < GC * GC; e += 256) {
     const int t = e / GC, j = e % GC;
-    if ((j >> 4) <= (t >> 4)) out[WS_AP + e] = ai[t * TP + j] * bt[j];
+    const bool up = (j >> 4) > (t >> 4);
+    out[WS_AP + e] = up ? 0.f : ai[t * TP + j] * bt[j];
+    if (up) out[WS_M + e] = 0.f;
   }
 }
 
@@ -290,8 +291,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   for (int e = tid; e < GR * GDK; e += 256) s_s[(e / GDK) * KP + e % GDK] = sin[e];
 
-  // one chunk ahead, in registers: the Ap and M runs (zero blocks above the diagonal are
-  // not read), Q and K row runs (bf16 inputs; f32 ones are read in the chunk, to stay
+  // one chunk ahead, in registers: the Ap and M runs, Q and K row runs (bf16 inputs; f32 ones are read in the chunk, to stay
   // within 256 registers), V at this lane's output positions, gam, tail
   float4 pap[4], pm[4];
   uint4 pq[4], pk[4];
@@ -304,18 +304,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // each operand's next-chunk load is issued right after its last use in this chunk, so
   // one set of registers serves both
   auto chunk_ws = [&](int ci) __attribute__((always_inline)) { return ws + ((int64_t)nh * nch + ci) * WS_CHUNK; };
-  const bool low = lg <= wave;  // the lane group's block is on or below the diagonal
+  // (no load is conditional: waits for loads are then counted exactly across the chunk loop)
   auto load_ap = [&](int ci) __attribute__((always_inline)) {
     const float *cw = chunk_ws(ci);
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      pap[u] = low ? *(const float4 *)&cw[WS_AP + tr * GC + 16 * lg + 4 * u] : float4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < 4; ++u) pap[u] = *(const float4 *)&cw[WS_AP + tr * GC + 16 * lg + 4 * u];
   };
   auto load_m = [&](int ci) __attribute__((always_inline)) {
     const float *cw = chunk_ws(ci);
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      pm[u] = low ? *(const float4 *)&cw[WS_M + tr * GC + 16 * lg + 4 * u] : float4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < 4; ++u) pm[u] = *(const float4 *)&cw[WS_M + tr * GC + 16 * lg + 4 * u];
   };
   auto load_q = [&](int ci) __attribute__((always_inline)) {  // Q, V, gam, tail
     const int t0 = ci * GC, n = T - t0 < GC ? T - t0 : GC;
@@ -355,8 +353,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   load_k(0);
   load_ap(0);
   load_m(0);
-  for (int ci = 0; ci < nch; ++ci) {
-    const int t0 = ci * GC, n = T - t0 < GC ? T - t0 : GC;
+  // one chunk; FULL chunks (all 64 steps within T) store every y row unconditionally
+  auto chunk = [&](int ci, auto full) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full)::value;
+    const int t0 = ci * GC, n = FULL ? GC : (T - t0 < GC ? T - t0 : GC);
     const int cn = ci + 1 < nch ? ci + 1 : ci;  // the next chunk (the last reloads itself)
     const bool live = tr < n;
     const float gq = live ? pg : 0.f, tl = live ? ptl : 0.f, gcl = pgl;
@@ -409,12 +409,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float db[16];
     lds_run<16>(db, &dt_s[li * TP + 16 * lg]);
     yacc = mm_rr<16>(yacc, (const float *)pm, db);
-    __builtin_amdgcn_sched_barrier(0);
-    load_m(cn);
 #pragma unroll
     for (int vv = 0; vv < 4; ++vv) {
       const int t = 16 * wave + 4 * lg + vv;
-      if (t < n) {
+      if (FULL || t < n) {
         const int64_t yi = (((int64_t)b * T + t0 + t) * Hv + hv) * Dv + r0 + li;
         if constexpr (Y_F32)
           ((float *)y)[yi] = yacc[vv];
@@ -436,7 +434,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int vv = 0; vv < 4; ++vv) s_s[(4 * lg + vv) * KP + 16 * (2 * wave + h) + li] = sacc[h][vv];
     }
-  }
+    // M for the next chunk after this chunk's y stores: memory operations complete in
+    // order, and a wait for a store (before its data register is reused) then does not
+    // also wait for these loads
+    __builtin_amdgcn_sched_barrier(0);
+    load_m(cn);
+  };
+  int ci = 0;
+  for (; ci < T / GC; ++ci) chunk(ci, std::true_type{});
+  if (ci < nch) chunk(ci, std::false_type{});  // the partial last chunk
   float *sout = st_out + ((int64_t)nh * Dv + r0) * GDK;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
