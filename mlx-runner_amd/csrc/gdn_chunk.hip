@@ -58,6 +58,15 @@ __device__ __forceinline__ f32x4 mm_rr(f32x4 c, const float *a, const float *b) 
   return c;
 }
 
+// As mm_rr on the bf16 MFMA (v_mfma_f32_16x16x32_bf16), 8 k per lane per instruction:
+// element e of a[m] and of b[m] in lane l pair up, whatever k they stand for.
+template <int NK>
+__device__ __forceinline__ f32x4 mm_bf(f32x4 c, const bf16x8_t *a, const bf16x8_t *b) {
+#pragma unroll
+  for (int m = 0; m < NK; ++m) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[m], b[m], c, 0, 0, 0);
+  return c;
+}
+
 // NK consecutive floats of LDS (16-byte aligned) into registers
 template <int NK>
 __device__ __forceinline__ void lds_run(float *o, const float *p) {
@@ -165,18 +174,33 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(const void *__restrict__ q
       for (int m = 0; m < 32; ++m) o[m] = 0.f;
     }
   };
+  auto row_run_bf = [&](const void *p, int t, bf16x8_t *o) __attribute__((always_inline)) {
+    const int tt = t < n ? t : n - 1;
+    const bf16x8_t *src = (const bf16x8_t *)((const uint16_t *)p + (((int64_t)b * T + t0 + tt) * Hk + hk) * GDK + 32 * lg);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) o[u] = t < n ? src[u] : bf16x8_t{};
+  };
   f32x4 kk[3], qk[3];
 #pragma unroll
   for (int s = 0; s < 3; ++s) {
     const int e = wave + 4 * s;
     if (e < 10) {
       const int tb = (e >= 1) + (e >= 3) + (e >= 6), jb = e - tb * (tb + 1) / 2;
-      float ka[32], qa[32], kb[32];
-      row_run(k, 16 * tb + li, ka);
-      row_run(q, 16 * tb + li, qa);
-      row_run(k, 16 * jb + li, kb);
-      kk[s] = mm_rr<32>(f32x4{0.f, 0.f, 0.f, 0.f}, ka, kb);
-      qk[s] = mm_rr<32>(f32x4{0.f, 0.f, 0.f, 0.f}, qa, kb);
+      if constexpr (IN_F32) {
+        float ka[32], qa[32], kb[32];
+        row_run(k, 16 * tb + li, ka);
+        row_run(q, 16 * tb + li, qa);
+        row_run(k, 16 * jb + li, kb);
+        kk[s] = mm_rr<32>(f32x4{0.f, 0.f, 0.f, 0.f}, ka, kb);
+        qk[s] = mm_rr<32>(f32x4{0.f, 0.f, 0.f, 0.f}, qa, kb);
+      } else {  // bf16 products are exact in f32: the bf16 MFMA, 32 k per instruction
+        bf16x8_t ka[4], qa[4], kb[4];
+        row_run_bf(k, 16 * tb + li, ka);
+        row_run_bf(q, 16 * tb + li, qa);
+        row_run_bf(k, 16 * jb + li, kb);
+        kk[s] = mm_bf<4>(f32x4{0.f, 0.f, 0.f, 0.f}, ka, kb);
+        qk[s] = mm_bf<4>(f32x4{0.f, 0.f, 0.f, 0.f}, qa, kb);
+      }
     }
   }
   __syncthreads();  // gd, bt
@@ -451,21 +475,257 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// x = hi + mid + lo exactly, each part bf16 (the truncation of what is left): x - hi keeps
+// at most 16 significant bits and is exact, mid takes the top 8 of them, and the rest (at
+// most 8 bits) is exact in bf16.  Returned as bf16 bit patterns.
+__device__ __forceinline__ void split3(float x, uint32_t &h, uint32_t &m, uint32_t &l) {
+  const uint32_t xb = __float_as_uint(x);
+  const float r1 = x - __uint_as_float(xb & 0xFFFF0000u);
+  const uint32_t rb = __float_as_uint(r1);
+  const float r2 = r1 - __uint_as_float(rb & 0xFFFF0000u);
+  h = xb >> 16;
+  m = rb >> 16;
+  l = __float_as_uint(r2) >> 16;
+}
+
+// bf16 LDS layout of the bf16-input scan (in bf16 elements): the state as three split
+// planes [GR][SPB]; K^T [GDK][.] with each 32-row band shifted by 32 elements (the four lane
+// groups' stores, rows 32 apart, then fall in distinct banks); (tail o Dl)^T as three split
+// planes [GR][DPB]
+constexpr int SPB = GDK + 8;
+constexpr int KTP = GC + 8;
+constexpr int DPB = GC + 8;
+__device__ __forceinline__ int ktb_at(int d, int t) { return d * KTP + 32 * (d >> 5) + t; }
+constexpr int KTB_SIZE = (GDK - 1) * KTP + 32 * (GDK / 32 - 1) + GC;
+constexpr size_t SCANB_LDS = (size_t)2 * GR * TP * 4 + (size_t)(3 * GR * SPB + KTB_SIZE + 3 * GR * DPB) * 2;
+
+// The scan for bf16 q, k, v.  Products with K or Q run on the bf16 MFMA, which multiplies
+// bf16 values exactly into f32: K S^T and Q S^T with S split into three bf16 planes, and
+// the state update Dl^T (tail o K) as (tail o Dl)^T split into three planes times K.  Each
+// f32 value is split once, by the lane that holds it.  Dl = Ap U and M Dl (f32 both sides)
+// stay on the f32 MFMA.  Layout, chunk loop and prefetch as in gdn_chunk_scan.
+template <bool Y_F32>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_chunk_scan_bf(
+    const void *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v, const float *__restrict__ ws,
+    const float *st_in, float *st_out, void *__restrict__ y, int T, int Hk, int Hv, int Dv, int nch) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float *u_s = lds, *dt_s = u_s + GR * TP;
+  uint16_t *sp = (uint16_t *)(dt_s + GR * TP), *ktb = sp + 3 * GR * SPB, *dp = ktb + KTB_SIZE;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  // workgroup id = head + heads * row group (a head's row groups share an XCD's L2)
+  const int nheads = gridDim.x / (Dv / GR);
+  const int nh = blockIdx.x % nheads, r0 = (blockIdx.x / nheads) * GR;
+  const int b = nh / Hv, hv = nh - b * Hv, hk = hv / (Hv / Hk);
+  const int tr = 16 * wave + li;
+
+  // the state rows r0 .. r0 + 15 in accumulators (tile h: row 4 (l / 16) + v, column
+  // 16 (2 w + h) + l % 16), and as split planes in LDS
+  const float *sin = st_in + ((int64_t)nh * Dv + r0) * GDK;
+  f32x4 sacc[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) sacc[h][vv] = sin[(4 * lg + vv) * GDK + 16 * (2 * wave + h) + li];
+  }
+  auto put_state = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int vv = 0; vv < 4; ++vv) {
+        uint32_t p0, p1, p2;
+        split3(sacc[h][vv], p0, p1, p2);
+        const int o = (4 * lg + vv) * SPB + 16 * (2 * wave + h) + li;
+        sp[o] = (uint16_t)p0;
+        sp[GR * SPB + o] = (uint16_t)p1;
+        sp[2 * GR * SPB + o] = (uint16_t)p2;
+      }
+    }
+  };
+  put_state();
+
+  // one chunk ahead, in registers: Q and K row runs (bf16, the A operands as they are), V
+  // and gam, tail at this lane's output rows, the Ap and M runs
+  bf16x8_t pq[4], pk[4];
+  float4 pap[4], pm[4], pg4, ptl4;
+  float pv[4], pgl;
+  auto qk_off = [&](int ci) __attribute__((always_inline)) {
+    const int t0 = ci * GC, n = T - t0 < GC ? T - t0 : GC;
+    const int tt = tr < n ? tr : n - 1;  // steps past T re-read the last one (scaled by 0)
+    return (((int64_t)b * T + t0 + tt) * Hk + hk) * GDK + 32 * lg;
+  };
+  auto chunk_ws = [&](int ci) __attribute__((always_inline)) { return ws + ((int64_t)nh * nch + ci) * WS_CHUNK; };
+  auto load_ap = [&](int ci) __attribute__((always_inline)) {
+    const float *cw = chunk_ws(ci);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pap[u] = *(const float4 *)&cw[WS_AP + tr * GC + 16 * lg + 4 * u];
+  };
+  auto load_m = [&](int ci) __attribute__((always_inline)) {
+    const float *cw = chunk_ws(ci);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pm[u] = *(const float4 *)&cw[WS_M + tr * GC + 16 * lg + 4 * u];
+  };
+  auto load_q = [&](int ci) __attribute__((always_inline)) {  // Q, V, gam, tail
+    const int t0 = ci * GC, n = T - t0 < GC ? T - t0 : GC;
+    const float *cw = chunk_ws(ci);
+    pg4 = *(const float4 *)&cw[WS_GAM + 16 * wave + 4 * lg];
+    ptl4 = *(const float4 *)&cw[WS_TAIL + 16 * wave + 4 * lg];
+    pgl = cw[WS_GAM + GC - 1];
+    const bf16x8_t *src = (const bf16x8_t *)((const uint16_t *)q + qk_off(ci));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pq[u] = src[u];
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) {
+      const int t = 16 * wave + 4 * lg + vv, tt = t < n ? t : n - 1;
+      pv[vv] = bf16_to_f32(((const uint16_t *)v)[(((int64_t)b * T + t0 + tt) * Hv + hv) * Dv + r0 + li]);
+    }
+  };
+  auto load_k = [&](int ci) __attribute__((always_inline)) {
+    const bf16x8_t *src = (const bf16x8_t *)((const uint16_t *)k + qk_off(ci));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pk[u] = src[u];
+  };
+
+  load_q(0);
+  load_k(0);
+  load_ap(0);
+  load_m(0);
+  // one chunk; FULL chunks (all 64 steps within T) store every y row unconditionally
+  auto chunk = [&](int ci, auto full) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full)::value;
+    const int t0 = ci * GC, n = FULL ? GC : (T - t0 < GC ? T - t0 : GC);
+    const int cn = ci + 1 < nch ? ci + 1 : ci;  // the next chunk (the last reloads itself)
+    // this lane's output rows t = 16 w + 4 (l / 16) + v: gam (0 past T), V, tail
+    float gv[4], uv[4];
+    const float tlv[4] = {ptl4.x, ptl4.y, ptl4.z, ptl4.w}, gw[4] = {pg4.x, pg4.y, pg4.z, pg4.w};
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) {
+      const bool live = FULL || 16 * wave + 4 * lg + vv < n;
+      gv[vv] = live ? gw[vv] : 0.f;
+      uv[vv] = live ? pv[vv] : 0.f;
+    }
+    const float gcl = pgl;
+    bf16x8_t ak[4], aq[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ak[u] = pk[u], aq[u] = pq[u];
+    __syncthreads();  // (A) the state planes hold the state before this chunk
+    load_q(cn);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // K S^T and Q S^T over this wave's 16 steps; U = V - gam o K S^T
+    f32x4 ur = {0.f, 0.f, 0.f, 0.f}, yr = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int o = li * SPB + 32 * lg + 8 * c;
+      const bf16x8_t s0 = *(const bf16x8_t *)&sp[o], s1 = *(const bf16x8_t *)&sp[GR * SPB + o],
+                     s2 = *(const bf16x8_t *)&sp[2 * GR * SPB + o];
+      ur = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[c], s0, ur, 0, 0, 0);
+      yr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq[c], s0, yr, 0, 0, 0);
+      ur = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[c], s1, ur, 0, 0, 0);
+      yr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq[c], s1, yr, 0, 0, 0);
+      ur = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[c], s2, ur, 0, 0, 0);
+      yr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq[c], s2, yr, 0, 0, 0);
+    }
+    f32x4 uacc, yacc;
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) {
+      uacc[vv] = __builtin_fmaf(-gv[vv], ur[vv], uv[vv]);
+      yacc[vv] = gv[vv] * yr[vv];
+    }
+    *(f32x4 *)&u_s[li * TP + 16 * wave + 4 * lg] = uacc;  // U^T
+    __syncthreads();  // (B) every wave's U rows are in u_s
+    // K^T of this lane's step row (bf16 as it is), the elements taken from the vector's
+    // 32-bit words (a __bf16 element read out of the vector with __builtin_bit_cast gave
+    // element 0 for all eight with this compiler); the next chunk's K then goes in flight
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4_t w = __builtin_bit_cast(u32x4_t, ak[c]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        ktb[ktb_at(32 * lg + 8 * c + e, tr)] = (uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
+    }
+    load_k(cn);
+    __builtin_amdgcn_sched_barrier(0);
+    // Dl = Ap U (f32)
+    float ub[16];
+    lds_run<16>(ub, &u_s[li * TP + 16 * lg]);
+    const f32x4 dl = mm_rr<16>(f32x4{0.f, 0.f, 0.f, 0.f}, (const float *)pap, ub);
+    __builtin_amdgcn_sched_barrier(0);
+    load_ap(cn);
+    *(f32x4 *)&dt_s[li * TP + 16 * wave + 4 * lg] = dl;  // Dl^T
+    {  // (tail o Dl)^T as split planes: row li, columns 16 w + 4 (l / 16) + v
+      uint32_t p0[4], p1[4], p2[4];
+#pragma unroll
+      for (int vv = 0; vv < 4; ++vv) split3(tlv[vv] * dl[vv], p0[vv], p1[vv], p2[vv]);
+      const int o = li * DPB + 16 * wave + 4 * lg;
+      *(uint2 *)&dp[o] = make_uint2(p0[0] | (p0[1] << 16), p0[2] | (p0[3] << 16));
+      *(uint2 *)&dp[GR * DPB + o] = make_uint2(p1[0] | (p1[1] << 16), p1[2] | (p1[3] << 16));
+      *(uint2 *)&dp[2 * GR * DPB + o] = make_uint2(p2[0] | (p2[1] << 16), p2[2] | (p2[3] << 16));
+    }
+    __syncthreads();  // (C) every wave's Dl rows are in dt_s and dp, all of K^T is written
+    // Y = gam o Q S^T + M Dl
+    float db[16];
+    lds_run<16>(db, &dt_s[li * TP + 16 * lg]);
+    yacc = mm_rr<16>(yacc, (const float *)pm, db);
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) {
+      const int t = 16 * wave + 4 * lg + vv;
+      if (FULL || t < n) {
+        const int64_t yi = (((int64_t)b * T + t0 + t) * Hv + hv) * Dv + r0 + li;
+        if constexpr (Y_F32)
+          ((float *)y)[yi] = yacc[vv];
+        else
+          ((uint16_t *)y)[yi] = f32_to_bf16_rne(yacc[vv]);
+      }
+    }
+    // S = gam_{C-1} S + (tail o Dl)^T K
+#pragma unroll
+    for (int h = 0; h < 2; ++h) sacc[h] *= gcl;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int o = li * DPB + 16 * lg + 8 * c;
+      const bf16x8_t a0 = *(const bf16x8_t *)&dp[o], a1 = *(const bf16x8_t *)&dp[GR * DPB + o],
+                     a2 = *(const bf16x8_t *)&dp[2 * GR * DPB + o];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bf16x8_t kb = *(const bf16x8_t *)&ktb[ktb_at(16 * (2 * wave + h) + li, 16 * lg + 8 * c)];
+        sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, kb, sacc[h], 0, 0, 0);
+        sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, kb, sacc[h], 0, 0, 0);
+        sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, kb, sacc[h], 0, 0, 0);
+      }
+    }
+    // every wave read the state planes before (B); the next chunk reads them after (A)
+    put_state();
+    // M for the next chunk after this chunk's y stores (memory operations complete in order)
+    __builtin_amdgcn_sched_barrier(0);
+    load_m(cn);
+  };
+  int ci = 0;
+  for (; ci < T / GC; ++ci) chunk(ci, std::true_type{});
+  if (ci < nch) chunk(ci, std::false_type{});  // the partial last chunk
+  float *sout = st_out + ((int64_t)nh * Dv + r0) * GDK;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) sout[(4 * lg + vv) * GDK + 16 * (2 * wave + h) + li] = sacc[h][vv];
+  }
+}
+
+// prep, then the scan (f32 inputs: gdn_chunk_scan; bf16 inputs: gdn_chunk_scan_bf); both
+// scans use under 64 KB of LDS, the default limit
 template <bool IN, bool YF>
 static hipError_t launch_chunked_t(const GdnArgs &a, float *ws, hipStream_t st) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)gdn_chunk_scan<IN, YF>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)SCAN_LDS);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static_assert(SCAN_LDS <= 65536 && SCANB_LDS <= 65536 && PREP_LDS <= 65536, "LDS over the default limit");
   const int nch = (a.T + GC - 1) / GC;
   const int64_t nh = (int64_t)a.B * a.Hv;
   hipLaunchKernelGGL((gdn_chunk_prep<IN>), dim3((unsigned)(nh * nch)), dim3(256), PREP_LDS, st, a.q, a.k, a.g, a.beta,
                      (int)a.beta_f32, ws, a.T, a.Hk, a.Hv, nch);
-  hipLaunchKernelGGL((gdn_chunk_scan<IN, YF>), dim3((unsigned)(nh * (a.Dv / GR))), dim3(256), SCAN_LDS, st, a.q, a.k,
-                     a.v, (const float *)ws, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv, nch);
+  if constexpr (IN)
+    hipLaunchKernelGGL((gdn_chunk_scan<true, YF>), dim3((unsigned)(nh * (a.Dv / GR))), dim3(256), SCAN_LDS, st, a.q,
+                       a.k, a.v, (const float *)ws, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv, nch);
+  else
+    hipLaunchKernelGGL((gdn_chunk_scan_bf<YF>), dim3((unsigned)(nh * (a.Dv / GR))), dim3(256), SCANB_LDS, st, a.q,
+                       a.k, a.v, (const float *)ws, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv, nch);
   return hipGetLastError();
 }
 
