@@ -36,12 +36,28 @@ constexpr int GR = 16;    // state rows per scan workgroup
 constexpr int KP = GDK + 4;  // LDS row pitch of [.][GDK] arrays (floats)
 constexpr int TP = GC + 4;   // LDS row pitch of [.][GC] arrays (16-byte aligned rows for float4 runs)
 
-// workspace per (b, hv, chunk), in floats (Ap and M in full, zero above the diagonal)
+// workspace per (b, hv, chunk), in floats: Ap and M (the 16 x 16 blocks on and below the
+// diagonal; blocks above it are read from one shared zero block at the end), gam, tail
 constexpr int WS_AP = 0;
 constexpr int WS_M = WS_AP + GC * GC;
 constexpr int WS_GAM = WS_M + GC * GC;
 constexpr int WS_TAIL = WS_GAM + GC;
 constexpr int WS_CHUNK = WS_TAIL + GC;
+constexpr int WS_ZERO = 64;  // the zero block's floats
+
+// Scan workgroup -> (b * Hv + hv, first state row).  Workgroups are dealt to the 8 XCDs in
+// turn (blockIdx % 8).  Those that read the same key head's q and k (Hv / Hk value heads x
+// Dv / 16 row groups) have consecutive linear indices, and each XCD takes a contiguous range
+// of them, so a key head's chunks are fetched into one XCD's L2 (and a value head's Ap, M
+// too).  False for the grid's padding workgroups (the grid is a multiple of 8).
+__device__ __forceinline__ bool scan_wg(int nwg, int nrg, int &nh, int &r0) {
+  const int per = (nwg + 7) / 8;
+  const int L = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (L >= nwg) return false;
+  nh = L / nrg;
+  r0 = (L - nh * nrg) * GR;
+  return true;
+}
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -266,13 +282,12 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(const void *__restrict__ q
     }
     __syncthreads();
   }
-  // Ap = A diag(beta); the blocks of Ap and M above the diagonal as zero
+  // Ap = A diag(beta), blocks on and below the diagonal; the shared zero block
   for (int e = tid; e < GC * GC; e += 256) {
     const int t = e / GC, j = e % GC;
-    const bool up = (j >> 4) > (t >> 4);
-    out[WS_AP + e] = up ? 0.f : ai[t * TP + j] * bt[j];
-    if (up) out[WS_M + e] = 0.f;
+    if ((j >> 4) <= (t >> 4)) out[WS_AP + e] = ai[t * TP + j] * bt[j];
   }
+  if (blockIdx.x == 0 && tid < WS_ZERO) ws[(int64_t)gridDim.x * WS_CHUNK + tid] = 0.f;
 }
 
 // (tail o K)^T in LDS: row d, column t, rows of each 32-row band shifted by 16 floats so
@@ -291,16 +306,13 @@ constexpr size_t SCAN_LDS = (size_t)(GR * KP + KT_SIZE + 2 * GR * TP) * 4;
 template <bool IN_F32, bool Y_F32>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_chunk_scan(
     const void *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v, const float *__restrict__ ws,
-    const float *st_in, float *st_out, void *__restrict__ y, int T, int Hk, int Hv, int Dv, int nch) {
+    const float *st_in, float *st_out, void *__restrict__ y, int T, int Hk, int Hv, int Dv, int nch, int nwg) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   float *s_s = lds, *kt_s = s_s + GR * KP, *u_s = kt_s + KT_SIZE, *dt_s = u_s + GR * TP;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;  // MFMA operand row / column, lane group
-  // workgroup id = head + heads * row group: the row groups of a head, which read the same
-  // chunk operands, are a multiple of the head count apart, so with a multiple of 8 heads
-  // they land on one XCD (workgroups are dealt to the 8 XCDs in turn) and share its L2
-  const int nheads = gridDim.x / (Dv / GR);
-  const int nh = blockIdx.x % nheads, r0 = (blockIdx.x / nheads) * GR;
+  int nh, r0;
+  if (!scan_wg(nwg, Dv / GR, nh, r0)) return;
   const int b = nh / Hv, hv = nh - b * Hv, hk = hv / (Hv / Hk);
   const int tr = 16 * wave + li;  // this lane's step row of the chunk for its A operands
 
@@ -328,16 +340,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // each operand's next-chunk load is issued right after its last use in this chunk, so
   // one set of registers serves both
   auto chunk_ws = [&](int ci) __attribute__((always_inline)) { return ws + ((int64_t)nh * nch + ci) * WS_CHUNK; };
-  // (no load is conditional: waits for loads are then counted exactly across the chunk loop)
+  // lane groups whose block is above the diagonal read the shared zero block instead (no
+  // load is conditional: waits for loads are then counted exactly across the chunk loop)
+  const bool low = lg <= wave;
+  const float *wz = ws + (int64_t)(nwg / (Dv / GR)) * nch * WS_CHUNK;
   auto load_ap = [&](int ci) __attribute__((always_inline)) {
     const float *cw = chunk_ws(ci);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) pap[u] = *(const float4 *)&cw[WS_AP + tr * GC + 16 * lg + 4 * u];
+    for (int u = 0; u < 4; ++u) pap[u] = ((const float4 *)(low ? &cw[WS_AP + tr * GC + 16 * lg] : wz))[u];
   };
   auto load_m = [&](int ci) __attribute__((always_inline)) {
     const float *cw = chunk_ws(ci);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) pm[u] = *(const float4 *)&cw[WS_M + tr * GC + 16 * lg + 4 * u];
+    for (int u = 0; u < 4; ++u) pm[u] = ((const float4 *)(low ? &cw[WS_M + tr * GC + 16 * lg] : wz))[u];
   };
   auto load_q = [&](int ci) __attribute__((always_inline)) {  // Q, V, gam, tail
     const int t0 = ci * GC, n = T - t0 < GC ? T - t0 : GC;
@@ -507,15 +522,14 @@ constexpr size_t SCANB_LDS = (size_t)2 * GR * TP * 4 + (size_t)(3 * GR * SPB + K
 template <bool Y_F32>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_chunk_scan_bf(
     const void *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v, const float *__restrict__ ws,
-    const float *st_in, float *st_out, void *__restrict__ y, int T, int Hk, int Hv, int Dv, int nch) {
+    const float *st_in, float *st_out, void *__restrict__ y, int T, int Hk, int Hv, int Dv, int nch, int nwg) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   float *u_s = lds, *dt_s = u_s + GR * TP;
   uint16_t *sp = (uint16_t *)(dt_s + GR * TP), *ktb = sp + 3 * GR * SPB, *dp = ktb + KTB_SIZE;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  // workgroup id = head + heads * row group (a head's row groups share an XCD's L2)
-  const int nheads = gridDim.x / (Dv / GR);
-  const int nh = blockIdx.x % nheads, r0 = (blockIdx.x / nheads) * GR;
+  int nh, r0;
+  if (!scan_wg(nwg, Dv / GR, nh, r0)) return;
   const int b = nh / Hv, hv = nh - b * Hv, hk = hv / (Hv / Hk);
   const int tr = 16 * wave + li;
 
@@ -554,16 +568,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int tt = tr < n ? tr : n - 1;  // steps past T re-read the last one (scaled by 0)
     return (((int64_t)b * T + t0 + tt) * Hk + hk) * GDK + 32 * lg;
   };
+  const bool low = lg <= wave;  // else the lane group's block is above the diagonal: the zero block
+  const float *wz = ws + (int64_t)(nwg / (Dv / GR)) * nch * WS_CHUNK;
   auto chunk_ws = [&](int ci) __attribute__((always_inline)) { return ws + ((int64_t)nh * nch + ci) * WS_CHUNK; };
   auto load_ap = [&](int ci) __attribute__((always_inline)) {
     const float *cw = chunk_ws(ci);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) pap[u] = *(const float4 *)&cw[WS_AP + tr * GC + 16 * lg + 4 * u];
+    for (int u = 0; u < 4; ++u) pap[u] = ((const float4 *)(low ? &cw[WS_AP + tr * GC + 16 * lg] : wz))[u];
   };
   auto load_m = [&](int ci) __attribute__((always_inline)) {
     const float *cw = chunk_ws(ci);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) pm[u] = *(const float4 *)&cw[WS_M + tr * GC + 16 * lg + 4 * u];
+    for (int u = 0; u < 4; ++u) pm[u] = ((const float4 *)(low ? &cw[WS_M + tr * GC + 16 * lg] : wz))[u];
   };
   auto load_q = [&](int ci) __attribute__((always_inline)) {  // Q, V, gam, tail
     const int t0 = ci * GC, n = T - t0 < GC ? T - t0 : GC;
@@ -720,12 +736,14 @@ static hipError_t launch_chunked_t(const GdnArgs &a, float *ws, hipStream_t st) 
   const int64_t nh = (int64_t)a.B * a.Hv;
   hipLaunchKernelGGL((gdn_chunk_prep<IN>), dim3((unsigned)(nh * nch)), dim3(256), PREP_LDS, st, a.q, a.k, a.g, a.beta,
                      (int)a.beta_f32, ws, a.T, a.Hk, a.Hv, nch);
+  const int nwg = (int)(nh * (a.Dv / GR));
+  const dim3 grid((unsigned)((nwg + 7) / 8 * 8));
   if constexpr (IN)
-    hipLaunchKernelGGL((gdn_chunk_scan<true, YF>), dim3((unsigned)(nh * (a.Dv / GR))), dim3(256), SCAN_LDS, st, a.q,
-                       a.k, a.v, (const float *)ws, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv, nch);
+    hipLaunchKernelGGL((gdn_chunk_scan<true, YF>), grid, dim3(256), SCAN_LDS, st, a.q, a.k, a.v, (const float *)ws,
+                       a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv, nch, nwg);
   else
-    hipLaunchKernelGGL((gdn_chunk_scan_bf<YF>), dim3((unsigned)(nh * (a.Dv / GR))), dim3(256), SCANB_LDS, st, a.q,
-                       a.k, a.v, (const float *)ws, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv, nch);
+    hipLaunchKernelGGL((gdn_chunk_scan_bf<YF>), grid, dim3(256), SCANB_LDS, st, a.q, a.k, a.v, (const float *)ws,
+                       a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv, nch, nwg);
   return hipGetLastError();
 }
 
@@ -735,12 +753,12 @@ bool gdn_chunked_ok(const GdnArgs &a) {
   if (a.Dk != GDK || a.Dv <= 0 || a.Dv % GR != 0 || a.Hk <= 0 || a.Hv % a.Hk != 0 || a.B <= 0) return false;
   if (a.T < GDN_CHUNKED_MIN_T) return false;
   const int64_t nch = (a.T + GC - 1) / GC, nh = (int64_t)a.B * a.Hv;
-  return nh * nch <= 0x7FFFFFFF && nh * (a.Dv / GR) <= 0x7FFFFFFF;
+  return nh * nch <= 0x7FFFFFFF && nh * (a.Dv / GR) <= 0x7FFFFFF0;
 }
 
 size_t gdn_chunked_workspace(const GdnArgs &a) {
   const int64_t nch = (a.T + GC - 1) / GC;
-  return (size_t)a.B * a.Hv * nch * WS_CHUNK * sizeof(float);
+  return ((size_t)a.B * a.Hv * nch * WS_CHUNK + WS_ZERO) * sizeof(float);
 }
 
 hipError_t launch_gdn_chunked(const GdnArgs &a, void *workspace, hipStream_t st) {
