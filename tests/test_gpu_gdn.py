@@ -175,14 +175,30 @@ def test_chunked_model_shapes(T):
     check(y, S, used)
 
 
-@pytest.mark.parametrize("dtypes", ["f32", "f32-beta-bf16-y-f32"])
+CHUNKED_KW = {"bf16": dict(),
+              "bf16-y-f32": dict(y_dtype=Q.FLOAT32),
+              "f32": dict(in_dtype=Q.FLOAT32, beta_dtype=Q.FLOAT32),
+              "f32-beta-bf16-y-f32": dict(in_dtype=Q.FLOAT32, beta_dtype=Q.BFLOAT16, y_dtype=Q.FLOAT32)}
+
+
+@pytest.mark.parametrize("dtypes", sorted(CHUNKED_KW))
 def test_chunked_dtypes_and_batches(dtypes):
     rng = np.random.default_rng(77)
     q, k, v, g, beta, st = model_inputs(rng, 2, 150, 2, 6, 32)
-    kw = {"f32": dict(in_dtype=Q.FLOAT32, beta_dtype=Q.FLOAT32),
-          "f32-beta-bf16-y-f32": dict(in_dtype=Q.FLOAT32, beta_dtype=Q.BFLOAT16, y_dtype=Q.FLOAT32)}[dtypes]
+    kw = CHUNKED_KW[dtypes]
     y, S, used = run(q, k, v, g, beta, st, **kw)
     check(y, S, used, y_bf16=kw.get("y_dtype", Q.BFLOAT16) == Q.BFLOAT16)
+
+
+@pytest.mark.parametrize("dtypes", ["bf16", "f32"])
+def test_chunked_grid_padding(dtypes):
+    """6 scan workgroups (3 heads x 2 row groups): the grid is rounded up to 8 and the two
+    extra workgroups exit; 130 steps leave a 2-step last chunk."""
+    rng = np.random.default_rng(79)
+    q, k, v, g, beta, st = model_inputs(rng, 1, 130, 1, 3, 32)
+    kw = CHUNKED_KW[dtypes]
+    y, S, used = run(q, k, v, g, beta, st, **kw)
+    check(y, S, used, y_bf16=True)
 
 
 def test_chunked_extreme_decays_and_gates():
