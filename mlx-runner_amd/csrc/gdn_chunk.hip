@@ -283,9 +283,12 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(const void *__restrict__ q
     __syncthreads();
   }
   // Ap = A diag(beta), blocks on and below the diagonal; the shared zero block
-  for (int e = tid; e < GC * GC; e += 256) {
-    const int t = e / GC, j = e % GC;
-    if ((j >> 4) <= (t >> 4)) out[WS_AP + e] = ai[t * TP + j] * bt[j];
+  for (int e = tid; e < GC * GC / 4; e += 256) {  // 4 consecutive columns per thread
+    const int t = e / (GC / 4), j = (e % (GC / 4)) * 4;
+    if ((j >> 4) <= (t >> 4)) {
+      const float4 av = *(const float4 *)&ai[t * TP + j], bv = *(const float4 *)&bt[j];
+      *(float4 *)&out[WS_AP + t * GC + j] = make_float4(av.x * bv.x, av.y * bv.y, av.z * bv.z, av.w * bv.w);
+    }
   }
   if (blockIdx.x == 0 && tid < WS_ZERO) ws[(int64_t)gridDim.x * WS_CHUNK + tid] = 0.f;
 }
