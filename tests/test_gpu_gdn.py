@@ -167,7 +167,7 @@ def test_argument_checks():
 
 # The chunked form (T >= 128): chunks of 64 steps on the f32 MFMA, the last chunk
 # padded with neutral steps; the same bar against the f64 oracle.
-@pytest.mark.parametrize("T", [128, 200, 1000])
+@pytest.mark.parametrize("T", [128, 200, 1000, 2048])
 def test_chunked_model_shapes(T):
     rng = np.random.default_rng(1000 + T)
     q, k, v, g, beta, st = model_inputs(rng, 1, T, 16, 48, 128)
