@@ -183,17 +183,19 @@ __global__ __launch_bounds__(256) void gdn_kernel(const void *__restrict__ q, co
   }
 }
 
-// T = 1 (a decode step): the same mapping and arithmetic as gdn_kernel (the results are equal
-// bit for bit), without the staging: each lane loads its own 8 elements of q and k, the row's
-// v and the head's g and beta straight from global memory together with its state, and the
-// lane that ends a row's reduction stores y.  No LDS and no barrier, so the step costs one
-// memory round trip.
+// T <= GDN_SHORT (a decode step, or the few steps of a speculative verify): the same mapping
+// and arithmetic as gdn_kernel (the results are equal bit for bit), without the staging: each
+// lane loads its own 8 elements of q and k, its row's v and the head's g and beta for every
+// step straight from global memory, all before the first step, together with its state, and
+// the lane that ends a row's reduction stores y.  No LDS and no barrier.
+constexpr int GDN_SHORT = 4;
+
 template <bool IN_F32, bool Y_F32>
-__global__ __launch_bounds__(256) void gdn_step1_kernel(const void *__restrict__ q, const void *__restrict__ k,
+__global__ __launch_bounds__(256) void gdn_short_kernel(const void *__restrict__ q, const void *__restrict__ k,
                                                         const void *__restrict__ v, const float *__restrict__ g,
                                                         const void *__restrict__ beta, int beta_f32,
                                                         const float *st_in, float *st_out, void *__restrict__ y,
-                                                        int Hk, int Hv, int Dv) {
+                                                        int T, int Hk, int Hv, int Dv) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int groups = (Dv + 15) >> 4;
   const int nh = blockIdx.x / groups, grp = blockIdx.x - nh * groups;  // nh = b * Hv + hv
@@ -204,42 +206,54 @@ __global__ __launch_bounds__(256) void gdn_step1_kernel(const void *__restrict__
   const int seg = (lane & 15) * 8;
   const int rr = live ? row : 0;
 
-  float s[8], qv[8], kv8[8];
+  float s[8];
   const int64_t so = ((int64_t)nh * Dv + rr) * GDN_DK + seg;
   {
     const float4 a = *(const float4 *)(st_in + so), c = *(const float4 *)(st_in + so + 4);
     s[0] = a.x, s[1] = a.y, s[2] = a.z, s[3] = a.w, s[4] = c.x, s[5] = c.y, s[6] = c.z, s[7] = c.w;
   }
-  const int64_t qk = ((int64_t)b * Hk + hk) * GDN_DK + seg;
-  ld8<IN_F32>(q, qk, qv);
-  ld8<IN_F32>(k, qk, kv8);
-  const float vt = ld_elem<IN_F32>(v, (int64_t)nh * Dv + rr);
-  const float gt = g[nh];
-  const float bt = beta_f32 ? ((const float *)beta)[nh] : bf16_to_f32(((const uint16_t *)beta)[nh]);
-
-  float kv = 0.f;
+  float qv[GDN_SHORT][8], kv8[GDN_SHORT][8], vt[GDN_SHORT], gt[GDN_SHORT], bt[GDN_SHORT];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    s[e] *= gt;
-    kv = __builtin_fmaf(s[e], kv8[e], kv);
-  }
-  kv = row16_sum(kv);
-  const float dlt = (vt - kv) * bt;
-  float o = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    s[e] = __builtin_fmaf(kv8[e], dlt, s[e]);
-    o = __builtin_fmaf(s[e], qv[e], o);
-  }
-  o = row16_sum(o);
-  if (live) {
-    if ((lane & 15) == 0) {
-      const int64_t yi = (int64_t)nh * Dv + row;
-      if constexpr (Y_F32)
-        ((float *)y)[yi] = o;
-      else
-        ((uint16_t *)y)[yi] = f32_to_bf16_rne(o);
+  for (int t = 0; t < GDN_SHORT; ++t) {
+    if (t < T) {
+      const int64_t bt_ = (int64_t)b * T + t;  // (batch, step)
+      const int64_t qk = (bt_ * Hk + hk) * GDN_DK + seg;
+      ld8<IN_F32>(q, qk, qv[t]);
+      ld8<IN_F32>(k, qk, kv8[t]);
+      vt[t] = ld_elem<IN_F32>(v, (bt_ * Hv + hv) * Dv + rr);
+      const int64_t gi = bt_ * Hv + hv;
+      gt[t] = g[gi];
+      bt[t] = beta_f32 ? ((const float *)beta)[gi] : bf16_to_f32(((const uint16_t *)beta)[gi]);
     }
+  }
+#pragma unroll
+  for (int t = 0; t < GDN_SHORT; ++t) {
+    if (t < T) {
+      float kv = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        s[e] *= gt[t];
+        kv = __builtin_fmaf(s[e], kv8[t][e], kv);
+      }
+      kv = row16_sum(kv);
+      const float dlt = (vt[t] - kv) * bt[t];
+      float o = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        s[e] = __builtin_fmaf(kv8[t][e], dlt, s[e]);
+        o = __builtin_fmaf(s[e], qv[t][e], o);
+      }
+      o = row16_sum(o);
+      if (live && (lane & 15) == 0) {
+        const int64_t yi = (((int64_t)b * T + t) * Hv + hv) * Dv + row;
+        if constexpr (Y_F32)
+          ((float *)y)[yi] = o;
+        else
+          ((uint16_t *)y)[yi] = f32_to_bf16_rne(o);
+      }
+    }
+  }
+  if (live) {
     *(float4 *)(st_out + so) = make_float4(s[0], s[1], s[2], s[3]);
     *(float4 *)(st_out + so + 4) = make_float4(s[4], s[5], s[6], s[7]);
   }
@@ -249,9 +263,9 @@ __global__ __launch_bounds__(256) void gdn_step1_kernel(const void *__restrict__
 
 template <bool IN, bool YF>
 static void launch_gdn_t(const GdnArgs &a, unsigned grid, hipStream_t st) {
-  if (a.T == 1)
-    hipLaunchKernelGGL((gdn_step1_kernel<IN, YF>), dim3(grid), dim3(256), 0, st, a.q, a.k, a.v, a.g, a.beta,
-                       (int)a.beta_f32, a.state_in, a.state_out, a.y, a.Hk, a.Hv, a.Dv);
+  if (a.T <= GDN_SHORT)
+    hipLaunchKernelGGL((gdn_short_kernel<IN, YF>), dim3(grid), dim3(256), 0, st, a.q, a.k, a.v, a.g, a.beta,
+                       (int)a.beta_f32, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv);
   else if (a.T <= GDN_TB)
     hipLaunchKernelGGL((gdn_kernel<IN, YF, true>), dim3(grid), dim3(256), 0, st, a.q, a.k, a.v, a.g, a.beta,
                        (int)a.beta_f32, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv);
