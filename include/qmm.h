@@ -128,7 +128,7 @@ int qmm_quantize(qmm_vector_array *res, qmm_array w, qmm_optional_int group_size
  * hv / (Hv / Hk).  Per step: S *= g; dlt = (v - S k) beta; S += dlt k^T; y = S q.
  * Results: y [B, T, Hv, Dv] in y_dtype (bfloat16 RNE or float32) and the final
  * state [B, Hv, Dv, Dk] float32.  state_out may be the state's own handle (the
- * update is then in place).  q, k and state must be 16-byte aligned.  From T = 128
+ * update is then in place).  q, k and state must be 16-byte aligned.  From T = 96
  * (with Dv % 16 == 0) the steps run in chunks of 64 as matrix products (the same
  * recurrence to f32 rounding), with a workspace of B * Hv * ceil(T / 64) * 33 KB
  * allocated on the stream and released after the call's kernels. */

@@ -111,7 +111,7 @@ struct GdnArgs {
 hipError_t launch_gdn(const GdnArgs &a, hipStream_t st);
 // The chunked form on the f32 MFMA, for long T: a per-chunk prep kernel writes its
 // matrices to `workspace` (gdn_chunked_workspace bytes), a scan kernel runs the chunks.
-constexpr int GDN_CHUNKED_MIN_T = 128;
+constexpr int GDN_CHUNKED_MIN_T = 96;
 bool gdn_chunked_ok(const GdnArgs &a);
 size_t gdn_chunked_workspace(const GdnArgs &a);
 hipError_t launch_gdn_chunked(const GdnArgs &a, void *workspace, hipStream_t st);
