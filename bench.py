@@ -13,8 +13,15 @@ launches).  The graph is replayed untimed until two consecutive replays agree
 within 3% (the clocks ramp over the first few hundred launches), then one
 replay is timed, bracketed by HIP events on the launch stream.
 
+With no --config, every workload the headline metric is quoted on is timed in
+turn (HEADLINE_SET: the gate+up GEMV first, whose figures are the line's
+`value`; the mxfp8 GEMV, the down projection at M = 1-3, the mxfp8 prefill
+GEMM, the lm_head GEMV and the lm_head prefill GEMM), each reported under
+`configs` with its own roofline and CPU baseline.
+
 Prints ONE JSON line on stdout.  The CPU baseline is the oracle's
-fp32-accumulating restatement, timed on the host on a bounded sample.
+fp32-accumulating restatement, timed on the host on a bounded sample on every
+thread of the job's CPU share.
 """
 from __future__ import annotations
 
@@ -128,13 +135,33 @@ def traffic_from_profiles(name):
     return None
 
 
-def cpu_baseline(cfg, xb, wq, s, budget_s=12.0):
-    """Oracle's fp32-accumulating qmm on host threads over a bounded sample of the workload."""
-    import numpy as np
+def host_threads():
+    """Host threads the CPU baseline may use, and how that number was found.
 
+    The job's CPU share is the smallest of the affinity mask, the cgroup CPU
+    quota and OMP_NUM_THREADS (a host that shares its CPUs among one-GPU jobs
+    grants each a fixed share and sets OMP_NUM_THREADS to it); os.cpu_count()
+    is reported beside it."""
+    n_aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    limits = {"affinity": n_aff}
+    try:
+        q, p = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            limits["cgroup_quota"] = max(1, int(int(q) // int(p)))
+    except (OSError, ValueError):
+        pass
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        limits["OMP_NUM_THREADS"] = max(1, int(os.environ["OMP_NUM_THREADS"]))
+    used = min(limits.values())
+    return used, dict(limits, os_cpu_count=os.cpu_count())
+
+
+def cpu_baseline(cfg, xb, wq, s, budget_s=4.0):
+    """Oracle's fp32-accumulating qmm on every host thread of the job's CPU share,
+    over a bounded sample of the workload."""
     import oracle as O
 
-    threads = min(16, os.cpu_count() or 1)
+    threads, limits = host_threads()
     M, N, K = cfg["M"], cfg["N"], cfg["K"]
     rows = N
     # for the compute-bound configs take a slice of output columns (full K, all M rows)
@@ -155,8 +182,10 @@ def cpu_baseline(cfg, xb, wq, s, budget_s=12.0):
         value, unit = alg["bytes"] / dt / 1e9, "GB/s"
     else:
         value, unit = alg["flops"] / dt / 1e12, "TFLOP/s"
+    share = ", ".join(f"{k}={v}" for k, v in limits.items())
     sample = (f"{reps} calls of M={M} x {rows} of {N} output rows, K={K} ({cfg['mode']}), "
-              f"{dt * 1e3:.2f} ms/call, {reps * dt:.1f} s total")
+              f"{dt * 1e3:.2f} ms/call, {reps * dt:.1f} s total; CPU restatement (not MLX) on {threads} threads "
+              f"= the job's CPU share ({share})")
     return dict(value=round(value, 4), unit=unit, cores=threads, kind="port", sample=sample,
                 us_per_call=round(dt * 1e6, 1))
 
@@ -413,56 +442,16 @@ def bench_census(args):
     print(json.dumps(line), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default=DEFAULT, choices=sorted(CONFIGS))
-    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--census", choices=("nvfp4", "mxfp8"),
-                    help="instead of one config, time every quantized linear of a decoded token in this mode")
-    ap.add_argument("--census-m", type=int, default=1, help="x rows for --census (1 decode, 2-3 MTP verify)")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="instead of the workload, run K plain 512 MiB -> 512 MiB copy kernels (torch.neg on "
-                         "float32) so HBM counters (FETCH_SIZE / WRITE_SIZE) can be scaled to known bytes")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this path runs on a single MI355X); got --gpus {args.gpus}",
-              file=sys.stderr)
-        sys.exit(2)
+# The workloads the headline metric is quoted on, in the order the default run
+# times them; the first is the headline `value`.
+HEADLINE_SET = ["gateup", "mxfp8_gemv", "down_m1", "down_m2", "down_m3", "prefill", "lmhead", "lmhead_prefill"]
+METRIC = "qmatmul GB/s & % HBM peak at M=1 (nvfp4/mxfp8); TFLOPS & % MFMA at M=4096"
 
-    import numpy as np
-    import torch
 
-    import qmm as Q
-
-    if args.copy_calibration:
-        n = 128 << 20  # float32 elements: 512 MiB read + 512 MiB written per launch
-        src = torch.ones(n, dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        for _ in range(args.steps):
-            torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_kernel": "torch.neg float32", "bytes_read_per_launch": n * 4,
-                          "bytes_written_per_launch": n * 4, "launches": args.steps}), flush=True)
-        return
-
-    if args.census:
-        return bench_census(args)
-    cfg = CONFIGS[args.config]
-    if cfg.get("gdn"):
-        return bench_gdn(args, cfg)
-    mode, M, N, K = cfg["mode"], cfg["M"], cfg["N"], cfg["K"]
-    alg = algorithmic(cfg)
-    torch.cuda.set_device(0)
-    dev = torch.device("cuda", 0)
+def make_weights(cfg, copies, Q, torch, stream, dev):
+    """`copies` distinct seeded weight matrices of the config, quantized on the device."""
+    mode, N, K = cfg["mode"], cfg["N"], cfg["K"]
     gen = torch.Generator(device=dev)
-    copies = max(1, math.ceil(ROTATE_BYTES / (alg["w"] + alg["s"])))
-    stream = Q.Stream.torch_current()
-
     weights = []
     for r in range(copies):
         gen.manual_seed(1000 + r)
@@ -471,22 +460,46 @@ def main():
             weights.append((Q.Array.from_torch(W), None))
             continue
         wq, sc = Q.quantize(Q.Array.from_torch(W), mode, stream=stream)
+        del W
         if cfg.get("mlp"):
             gen.manual_seed(2000 + r)
             W2 = (torch.randn((N, K), generator=gen, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
             wq2, sc2 = Q.quantize(Q.Array.from_torch(W2), mode, stream=stream)
             weights.append((wq, sc, wq2, sc2))
-            del W, W2
+            del W2
             continue
         weights.append((wq, sc))
-        del W
+    return weights
+
+
+def measure_qmm(name, args, cache):
+    """Time one quantized-linear config; returns its result dict (the JSON line's fields)."""
+    import numpy as np
+    import torch
+
+    import qmm as Q
+
+    cfg = CONFIGS[name]
+    mode, M, N, K = cfg["mode"], cfg["M"], cfg["N"], cfg["K"]
+    alg = algorithmic(cfg)
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    copies = max(1, math.ceil(ROTATE_BYTES / (alg["w"] + alg["s"])))
+    stream = Q.Stream.torch_current()
+    key = (mode, N, K, bool(cfg.get("mlp")), copies)
+    if cache.get("key") != key:  # configs on the same weights (lm_head decode and prefill) share them
+        cache.clear()
+        torch.cuda.empty_cache()
+        cache["key"], cache["weights"] = key, make_weights(cfg, copies, Q, torch, stream, dev)
+    weights = cache["weights"]
+    gen = torch.Generator(device=dev)
     gen.manual_seed(7)
     xt = (torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32) * cfg["xscale"]).to(torch.bfloat16)
     x = Q.Array.from_torch(xt)
     yt = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     y = Q.Array.from_torch(yt)
     torch.cuda.synchronize()
-    print(f"[bench] {args.config}: {cfg['workload']}; {copies} weight copies, steps={args.steps} "
+    print(f"[bench] {name}: {cfg['workload']}; {copies} weight copies, steps={args.steps} "
           f"warmup={args.warmup}", file=sys.stderr, flush=True)
 
     def step(i, st):
@@ -504,69 +517,95 @@ def main():
         step(i, stream)
     torch.cuda.synchronize()
 
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if args.no_graph:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         start.record()
         for i in range(args.steps):
             step(i, stream)
         end.record()
         end.synchronize()
+        ms = start.elapsed_time(end) / args.steps
     else:
-        g = torch.cuda.CUDAGraph()
-        cap = torch.cuda.Stream()
-        cap.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(cap):
-            cst = Q.Stream.torch_current()
-            step(0, cst)  # one eager call on the capture stream before capture
-            torch.cuda.current_stream().synchronize()
-            with torch.cuda.graph(g, stream=cap):
-                for i in range(args.steps):
-                    step(i, Q.Stream.torch_current())
-        torch.cuda.synchronize()
-        # Settle: the GPU's clocks ramp over the first few hundred back-to-back
-        # launches (measured: ~23 us -> ~19 us per call on the gate+up GEMV), so
-        # replay untimed until two consecutive replays agree within 3% (<= ~0.5 s).
-        prev, t_end = None, time.perf_counter() + 0.5
-        while True:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            g.replay()
-            e1.record()
-            e1.synchronize()
-            cur = e0.elapsed_time(e1)
-            if (prev is not None and abs(cur - prev) <= 0.03 * prev) or time.perf_counter() > t_end:
-                break
-            prev = cur
-        torch.cuda.synchronize()
-        start.record()
-        g.replay()
-        end.record()
-        end.synchronize()
-    ms_total = start.elapsed_time(end)
-    ms = ms_total / args.steps
-    sec = ms / 1e3
-    roof = roofline_of(cfg, alg, sec)
-    roof["traffic"] = traffic_from_profiles(args.config)
+        ms = replay_timed(step, args.steps)
+    roof = roofline_of(cfg, alg, ms / 1e3)
+    roof["traffic"] = traffic_from_profiles(name)
 
     cpu = None
     if not args.no_cpu and mode != "bf16" and not cfg.get("mlp"):
         wq0, sc0 = weights[0]
-        cpu = cpu_baseline(cfg, xt.view(torch.int16).cpu().numpy().view(np.uint16), wq0.numpy(), sc0.numpy())
-
-    metric = "qmatmul GB/s & % HBM peak at M=1 (nvfp4/mxfp8); TFLOPS & % MFMA at M=4096"
-    unit, value = roof["unit"], roof["achieved"]
-    line = {
-        "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 5), "us_per_call": round(ms * 1e3, 2), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None,
+        cpu = cpu_baseline(cfg, xt.view(torch.int16).cpu().numpy().view(np.uint16), wq0.numpy(), sc0.numpy(),
+                           budget_s=args.cpu_budget)
+    print(f"[bench] {name}: {ms * 1e3:.2f} us/call, {roof['achieved']} {roof['unit']} ({roof['frac']:.3f} of "
+          f"{roof['peak']:.0f})" + (f"; CPU {cpu['value']} {cpu['unit']} on {cpu['cores']} threads" if cpu else ""),
+          file=sys.stderr, flush=True)
+    return {
+        "name": name, "ms_per_step": round(ms, 5), "us_per_call": round(ms * 1e3, 2),
         "dtype": "bf16 (fp32 accumulate)" if mode == "bf16" else f"{mode} weights x bf16 (fp32 accumulate)",
-        "data": "synthetic (seeded N(0,1) x, N(0,0.02) W quantized on device)",
         "config": {"workload": cfg["workload"], "mode": mode, "M": M, "N": N, "K": K, "weight_copies": copies,
                    "algorithmic_bytes": alg["bytes"], "algorithmic_flops": alg["flops"],
                    "timing": "eager" if args.no_graph else "hip graph replay"},
         "roofline": roof, "cpu_baseline": cpu,
     }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", default=None, choices=sorted(CONFIGS),
+                    help="time one workload (default: every headline workload, the gate+up GEMV first)")
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-budget", type=float, default=4.0, help="seconds of CPU baseline per workload")
+    ap.add_argument("--census", choices=("nvfp4", "mxfp8"),
+                    help="instead of one config, time every quantized linear of a decoded token in this mode")
+    ap.add_argument("--census-m", type=int, default=1, help="x rows for --census (1 decode, 2-3 MTP verify)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="instead of the workload, run K plain 512 MiB -> 512 MiB copy kernels (torch.neg on "
+                         "float32) so HBM counters (FETCH_SIZE / WRITE_SIZE) can be scaled to known bytes")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this path runs on a single MI355X); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import qmm as Q  # noqa: F401  (loads libqmm.so; fails loudly if it is not built)
+
+    if args.copy_calibration:
+        n = 128 << 20  # float32 elements: 512 MiB read + 512 MiB written per launch
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_kernel": "torch.neg float32", "bytes_read_per_launch": n * 4,
+                          "bytes_written_per_launch": n * 4, "launches": args.steps}), flush=True)
+        return
+
+    if args.census:
+        return bench_census(args)
+    if args.config and CONFIGS[args.config].get("gdn"):
+        return bench_gdn(args, CONFIGS[args.config])
+    names = [args.config] if args.config else HEADLINE_SET
+    cache = {}
+    results = [measure_qmm(n, args, cache) for n in names]
+    cache.clear()
+    head = results[0]
+    line = {
+        "metric": METRIC, "value": head["roofline"]["achieved"], "unit": head["roofline"]["unit"], "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["ms_per_step"],
+        "us_per_call": head["us_per_call"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": head["dtype"], "data": "synthetic (seeded N(0,1) x, N(0,0.02) W quantized on device)",
+        "config": head["config"], "roofline": head["roofline"], "cpu_baseline": head["cpu_baseline"],
+    }
+    if len(results) > 1:
+        line["configs"] = [{k: r[k] for k in ("name", "us_per_call", "dtype", "config", "roofline", "cpu_baseline")}
+                           for r in results]
     print(json.dumps(line), flush=True)
 
 
