@@ -128,10 +128,14 @@ int qmm_quantize(qmm_vector_array *res, qmm_array w, qmm_optional_int group_size
  * hv / (Hv / Hk).  Per step: S *= g; dlt = (v - S k) beta; S += dlt k^T; y = S q.
  * Results: y [B, T, Hv, Dv] in y_dtype (bfloat16 RNE or float32) and the final
  * state [B, Hv, Dv, Dk] float32.  state_out may be the state's own handle (the
- * update is then in place).  q, k and state must be 16-byte aligned.  From T = 96
- * (with Dv % 16 == 0) the steps run in chunks of 64 as matrix products (the same
- * recurrence to f32 rounding), with a workspace of B * Hv * ceil(T / 64) * 33 KB
- * allocated on the stream and released after the call's kernels. */
+ * update is then in place).  q, k and state must be 16-byte aligned.  g must lie
+ * in [0, 1] (the model's decays exp(-softplus(.) * A) do): a NaN g gives NaN in y
+ * from its step on (in the chunked form below, from the first step of its 64-step
+ * chunk) and in the state; a negative g gives NaN likewise in the chunked form.
+ * From T = 96 (with Dv % 16 == 0) the steps run in chunks of 64 as matrix products
+ * (the same recurrence to f32 rounding for g in [0, 1]), with a workspace of
+ * B * Hv * ceil(T / 64) * 33 KB allocated on the stream and released after the
+ * call's kernels. */
 int qmm_gdn_recurrence(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_array k, qmm_array v, qmm_array g,
                        qmm_array beta, qmm_array state, qmm_dtype y_dtype, qmm_stream s);
 

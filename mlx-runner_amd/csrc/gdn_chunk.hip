@@ -162,7 +162,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(const void *__restrict__ q
     if (lane < n) {
       const int64_t gi = ((int64_t)b * T + t0 + lane) * Hv + hv;
       const double gv = (double)g[gi];
-      a = gv > 0.0 ? log(gv) : -1.0e4;  // g = 0 wipes the state: exp of the difference underflows to 0
+      // g = 0 (either sign) wipes the state: exp of the difference underflows to 0.  A NaN or
+      // negative g gives NaN from that step on, as the step kernel's multiply by g gives NaN
+      // for a NaN g (a negative g, outside the model's (0, 1], has no logarithm).
+      a = gv > 0.0 ? log(gv) : (gv == 0.0 ? -1.0e4 : __longlong_as_double(0x7FF8000000000000LL));
       be = beta_f32 ? ((const float *)beta)[gi] : bf16_to_f32(((const uint16_t *)beta)[gi]);
     }
 #pragma unroll

@@ -236,3 +236,20 @@ def test_long_T_rows_not_multiple_of_16_step_kernel():
     q, k, v, g, beta, st = model_inputs(rng, 1, 160, 2, 4, 24)
     y, S, used = run(q, k, v, g, beta, st)
     check(y, S, used)
+
+
+@pytest.mark.parametrize("T", [95, 96, 200])
+def test_nan_decay_propagates(T):
+    """A NaN g at one step of one head: NaN in that head's y from the step on and in its
+    state, in the step kernel (T < 96) and in the chunked form (T >= 96), where it also
+    reaches the earlier steps of its 64-step chunk; every other head stays finite."""
+    rng = np.random.default_rng(T)
+    q, k, v, g, beta, st = model_inputs(rng, 1, T, 2, 6, 16)
+    g[0, 70 if T > 96 else 40, 3] = np.nan
+    t_nan = 70 if T > 96 else 40
+    y, S, _ = run(q, k, v, g, beta, st)
+    assert np.isnan(y[0, t_nan:, 3]).all() and np.isnan(S[0, 3]).all()
+    others = [h for h in range(6) if h != 3]
+    assert np.isfinite(y[..., others, :]).all() and np.isfinite(S[:, others]).all()
+    first = t_nan if T < 96 else t_nan // 64 * 64  # steps before this one are finite
+    assert np.isfinite(y[0, :first, 3]).all()
