@@ -139,6 +139,22 @@ int qmm_quantize(qmm_vector_array *res, qmm_array w, qmm_optional_int group_size
 int qmm_gdn_recurrence(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_array k, qmm_array v, qmm_array g,
                        qmm_array beta, qmm_array state, qmm_dtype y_dtype, qmm_stream s);
 
+/* qmm_gdn_recurrence without any allocation.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Arguments and results as in
+ * qmm_gdn_recurrence, except that *y and *state_out must already hold arrays of the
+ * results' shapes and dtypes ([B, T, Hv, Dv] y_dtype; [B, Hv, Dv, Dk] float32, which
+ * may be the state's own handle); otherwise the call fails and allocates nothing.
+ * The chunked form's workspace (T >= 96) is a 64 MiB array in the library, one per
+ * GPU, held until the process ends: a call whose workspace is larger runs as several
+ * launches (groups of whole batches, or runs of whole 64-step chunks of one batch),
+ * with results identical bit for bit to one launch; Hv above 2016 value heads (one
+ * 64-step chunk of one batch over all of them exceeds the array) is rejected.  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (on
+ * different streams, or from different threads) race and give wrong results. */
+int qmm_gdn_recurrence_noalloc(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_array k, qmm_array v,
+                               qmm_array g, qmm_array beta, qmm_array state, qmm_dtype y_dtype, qmm_stream s);
+
 /* silu(g) * u element-wise, with mlx-runner's per-op roundings in the arrays' dtype
  * (bfloat16 or float32): sg = sigmoid(g), sl = g * sg, h = sl * u, each rounded
  * (silu src/model.zig:405-415, mul :451-456).  g and u must have equal shapes. */

@@ -21,6 +21,7 @@
 // gdn_chunk_scan, one workgroup per (b, hv, 16 state rows): the chunks in
 // order; the rows' state stays in MFMA accumulators (wave w holds columns
 // 32 w .. 32 w + 31), and per chunk the products above run as 16 x 16 MFMA tiles.
+#include <mutex>
 #include <type_traits>
 
 #include "qmm_device.h"
@@ -755,23 +756,116 @@ static hipError_t launch_chunked_t(const GdnArgs &a, float *ws, hipStream_t st) 
 
 }  // namespace
 
-bool gdn_chunked_ok(const GdnArgs &a) {
-  if (a.Dk != GDK || a.Dv <= 0 || a.Dv % GR != 0 || a.Hk <= 0 || a.Hv % a.Hk != 0 || a.B <= 0) return false;
-  if (a.T < GDN_CHUNKED_MIN_T) return false;
+// The shapes the chunked kernels take, at any T >= 1.
+static bool gdn_chunked_shape_ok(const GdnArgs &a) {
+  if (a.Dk != GDK || a.Dv <= 0 || a.Dv % GR != 0 || a.Hk <= 0 || a.Hv % a.Hk != 0 || a.B <= 0 || a.T <= 0)
+    return false;
   const int64_t nch = (a.T + GC - 1) / GC, nh = (int64_t)a.B * a.Hv;
   return nh * nch <= 0x7FFFFFFF && nh * (a.Dv / GR) <= 0x7FFFFFF0;
 }
+
+bool gdn_chunked_ok(const GdnArgs &a) { return a.T >= GDN_CHUNKED_MIN_T && gdn_chunked_shape_ok(a); }
 
 size_t gdn_chunked_workspace(const GdnArgs &a) {
   const int64_t nch = (a.T + GC - 1) / GC;
   return ((size_t)a.B * a.Hv * nch * WS_CHUNK + WS_ZERO) * sizeof(float);
 }
 
-hipError_t launch_gdn_chunked(const GdnArgs &a, void *workspace, hipStream_t st) {
-  if (!gdn_chunked_ok(a)) return hipErrorInvalidValue;
-  float *ws = (float *)workspace;
+static hipError_t launch_chunked_any(const GdnArgs &a, float *ws, hipStream_t st) {
   if (a.in_f32) return a.y_f32 ? launch_chunked_t<true, true>(a, ws, st) : launch_chunked_t<true, false>(a, ws, st);
   return a.y_f32 ? launch_chunked_t<false, true>(a, ws, st) : launch_chunked_t<false, false>(a, ws, st);
+}
+
+hipError_t launch_gdn_chunked(const GdnArgs &a, void *workspace, hipStream_t st) {
+  if (!gdn_chunked_ok(a)) return hipErrorInvalidValue;
+  return launch_chunked_any(a, (float *)workspace, st);
+}
+
+// ---------------------------------------------------------------- the allocation-free form
+//
+// The workspace of qmm_gdn_recurrence_noalloc: one array per GPU, held by the process
+// until it ends.  Host code reaches it only through the address hipGetSymbolAddress
+// returns on each device (the array's name is not a device address on the host).
+constexpr size_t GDN_SCRATCH_BYTES = (size_t)64 << 20;
+static __device__ __align__(256) float scratch[GDN_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mtx;
+void *g_scratch_ptr[MAX_DEVICES] = {};
+}  // namespace
+
+size_t gdn_noalloc_scratch_bytes() { return GDN_SCRATCH_BYTES; }
+
+// Largest (b, hv, chunk) count one launch can take in the array.
+static int64_t scratch_chunks() { return (int64_t)(GDN_SCRATCH_BYTES / sizeof(float) - WS_ZERO) / WS_CHUNK; }
+
+bool gdn_noalloc_fits(const GdnArgs &a) { return (int64_t)a.Hv <= scratch_chunks(); }
+
+// The array's address on the current device, looked up once per device.
+static hipError_t noalloc_scratch(float **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mtx);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = (float *)g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
+// Arguments of the sub-problem: batches [b0, b0 + nb), steps [t0, t0 + nt).  A sub-problem
+// with nt < T has nb = 1, so its rows of q, k, v, g, beta and y are contiguous.
+static GdnArgs gdn_part(const GdnArgs &a, int b0, int nb, int t0, int nt) {
+  GdnArgs p = a;
+  const size_t ie = a.in_f32 ? 4 : 2, be = a.beta_f32 ? 4 : 2, ye = a.y_f32 ? 4 : 2;
+  const int64_t step0 = (int64_t)b0 * a.T + t0;  // first (b, t) row of the part
+  p.B = nb;
+  p.T = nt;
+  p.q = (const char *)a.q + step0 * a.Hk * a.Dk * ie;
+  p.k = (const char *)a.k + step0 * a.Hk * a.Dk * ie;
+  p.v = (const char *)a.v + step0 * a.Hv * a.Dv * ie;
+  p.g = a.g + step0 * a.Hv;
+  p.beta = (const char *)a.beta + step0 * a.Hv * be;
+  p.y = (char *)a.y + step0 * a.Hv * a.Dv * ye;
+  const int64_t s0 = (int64_t)b0 * a.Hv * a.Dv * a.Dk;
+  p.state_in = a.state_in + s0;
+  p.state_out = a.state_out + s0;
+  return p;
+}
+
+// The recurrence at T >= GDN_CHUNKED_MIN_T with the workspace in the array.  A call whose
+// workspace exceeds the array runs as several launches on the same stream: groups of whole
+// batches, or for one batch, runs of whole 64-step chunks, the state carried through
+// state_out.  Every (b, hv, chunk) is computed by the same instructions as in one launch,
+// so the results are identical bit for bit.  Needs gdn_noalloc_fits(a).
+hipError_t launch_gdn_chunked_noalloc(const GdnArgs &a, hipStream_t st) {
+  if (!gdn_chunked_ok(a) || !gdn_noalloc_fits(a)) return hipErrorInvalidValue;
+  float *ws = nullptr;
+  hipError_t e = noalloc_scratch(&ws);
+  if (e != hipSuccess) return e;
+  const int64_t cap = scratch_chunks(), nch = (a.T + GC - 1) / GC, per_batch = (int64_t)a.Hv * nch;
+  if ((int64_t)a.B * per_batch <= cap) return launch_chunked_any(a, ws, st);
+  if (per_batch <= cap) {  // groups of whole batches
+    const int group = (int)(cap / per_batch);
+    for (int b0 = 0; b0 < a.B && e == hipSuccess; b0 += group)
+      e = launch_chunked_any(gdn_part(a, b0, a.B - b0 < group ? a.B - b0 : group, 0, a.T), ws, st);
+    return e;
+  }
+  const int seg = (int)(cap / a.Hv) * GC;  // steps per launch, whole chunks
+  for (int b = 0; b < a.B && e == hipSuccess; ++b)
+    for (int t0 = 0; t0 < a.T && e == hipSuccess; t0 += seg) {
+      GdnArgs p = gdn_part(a, b, 1, t0, a.T - t0 < seg ? a.T - t0 : seg);
+      if (t0 > 0) p.state_in = p.state_out;  // the state the previous run left
+      e = launch_chunked_any(p, ws, st);
+    }
+  return e;
 }
 
 }  // namespace qmm

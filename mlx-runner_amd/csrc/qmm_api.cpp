@@ -637,64 +637,120 @@ int qmm_silu_mul(qmm_array *res, qmm_array g, qmm_array u, qmm_stream s) {
   return finish(0);
 }
 
+// Validates the arguments of the GDN recurrence (shapes and dtypes of gdnKernelRun's
+// inputs, src/model.zig:284-319, and fusedEligible, :322-329) into *a, all but the
+// output pointers.  Returns 0, or non-zero with the error latched.
+static int gdn_args(const char *op, qmm_array q, qmm_array k, qmm_array v, qmm_array g, qmm_array beta,
+                    qmm_array state, qmm_dtype y_dtype, GdnArgs *a) {
+  Arr *qa = (Arr *)q.ctx, *ka = (Arr *)k.ctx, *va = (Arr *)v.ctx, *ga = (Arr *)g.ctx, *ba = (Arr *)beta.ctx,
+      *sa = (Arr *)state.ctx;
+  if (!qa || !ka || !va || !ga || !ba || !sa) return fail("[%s] missing input", op);
+  if (qa->ndim != 4 || ka->ndim != 4 || va->ndim != 4 || sa->ndim != 4)
+    return fail("[%s] q, k, v and state must be 4-D", op);
+  const int B = qa->shape[0], T = qa->shape[1], Hk = qa->shape[2], Dk = qa->shape[3];
+  const int Hv = va->shape[2], Dv = va->shape[3];
+  for (int i = 0; i < 4; ++i)
+    if (ka->shape[i] != qa->shape[i]) return fail("[%s] q and k shapes differ", op);
+  if (va->shape[0] != B || va->shape[1] != T) return fail("[%s] v must be [B, T, Hv, Dv]", op);
+  if (ga->ndim != 3 || ga->shape[0] != B || ga->shape[1] != T || ga->shape[2] != Hv)
+    return fail("[%s] g must be [B, T, Hv]", op);
+  if (ba->ndim != 3 || ba->shape[0] != B || ba->shape[1] != T || ba->shape[2] != Hv)
+    return fail("[%s] beta must be [B, T, Hv]", op);
+  if (sa->shape[0] != B || sa->shape[1] != Hv || sa->shape[2] != Dv || sa->shape[3] != Dk)
+    return fail("[%s] state must be [B, Hv, Dv, Dk]", op);
+  if (qa->dtype != ka->dtype || qa->dtype != va->dtype || (qa->dtype != QMM_BFLOAT16 && qa->dtype != QMM_FLOAT32))
+    return fail("[%s] q, k, v must all be bfloat16 or all float32", op);
+  if (ga->dtype != QMM_FLOAT32 || sa->dtype != QMM_FLOAT32) return fail("[%s] g and state must be float32", op);
+  if (ba->dtype != QMM_BFLOAT16 && ba->dtype != QMM_FLOAT32) return fail("[%s] beta must be bfloat16 or float32", op);
+  if (y_dtype != QMM_BFLOAT16 && y_dtype != QMM_FLOAT32) return fail("[%s] y must be bfloat16 or float32", op);
+  if (Dk != 128 || Dv <= 0 || Dv % 8 != 0 || Hk <= 0 || Hv % Hk != 0)
+    return fail("[%s] needs Dk = 128, Dv a multiple of 8 and Hv a multiple of Hk (got Dk %d, Dv %d, Hk %d, Hv %d)",
+                op, Dk, Dv, Hk, Hv);
+  if ((((uintptr_t)qa->data) | ((uintptr_t)ka->data) | ((uintptr_t)sa->data)) & 15)
+    return fail("[%s] q, k and state must be 16-byte aligned", op);
+  a->B = B, a->T = T, a->Hk = Hk, a->Hv = Hv, a->Dk = Dk, a->Dv = Dv;
+  a->in_f32 = qa->dtype == QMM_FLOAT32;
+  a->beta_f32 = ba->dtype == QMM_FLOAT32;
+  a->y_f32 = y_dtype == QMM_FLOAT32;
+  a->q = qa->data, a->k = ka->data, a->v = va->data, a->beta = ba->data;
+  a->g = (const float *)ga->data, a->state_in = (const float *)sa->data;
+  a->state_out = nullptr, a->y = nullptr;
+  return 0;
+}
+
+// T = 0: no steps, the state passes through (a copy unless the update is in place).
+static hipError_t gdn_no_steps(const GdnArgs &a, hipStream_t st) {
+  if (a.state_out == a.state_in) return hipSuccess;
+  const size_t bytes = (size_t)a.B * a.Hv * a.Dv * a.Dk * sizeof(float);
+  return hipMemcpyAsync(a.state_out, a.state_in, bytes, hipMemcpyDeviceToDevice, st);
+}
+
 int qmm_gdn_recurrence(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_array k, qmm_array v, qmm_array g,
                        qmm_array beta, qmm_array state, qmm_dtype y_dtype, qmm_stream s) {
   const char *op = "gdn_recurrence";
   if (!y || !state_out) return finish(fail("[%s] null result pointer", op));
-  Arr *qa = (Arr *)q.ctx, *ka = (Arr *)k.ctx, *va = (Arr *)v.ctx, *ga = (Arr *)g.ctx, *ba = (Arr *)beta.ctx,
-      *sa = (Arr *)state.ctx;
-  if (!qa || !ka || !va || !ga || !ba || !sa) return finish(fail("[%s] missing input", op));
-  // shapes and dtypes of gdnKernelRun's inputs (src/model.zig:284-319) and fusedEligible (:322-329)
-  if (qa->ndim != 4 || ka->ndim != 4 || va->ndim != 4 || sa->ndim != 4)
-    return finish(fail("[%s] q, k, v and state must be 4-D", op));
-  const int B = qa->shape[0], T = qa->shape[1], Hk = qa->shape[2], Dk = qa->shape[3];
-  const int Hv = va->shape[2], Dv = va->shape[3];
-  for (int i = 0; i < 4; ++i)
-    if (ka->shape[i] != qa->shape[i]) return finish(fail("[%s] q and k shapes differ", op));
-  if (va->shape[0] != B || va->shape[1] != T) return finish(fail("[%s] v must be [B, T, Hv, Dv]", op));
-  if (ga->ndim != 3 || ga->shape[0] != B || ga->shape[1] != T || ga->shape[2] != Hv)
-    return finish(fail("[%s] g must be [B, T, Hv]", op));
-  if (ba->ndim != 3 || ba->shape[0] != B || ba->shape[1] != T || ba->shape[2] != Hv)
-    return finish(fail("[%s] beta must be [B, T, Hv]", op));
-  if (sa->shape[0] != B || sa->shape[1] != Hv || sa->shape[2] != Dv || sa->shape[3] != Dk)
-    return finish(fail("[%s] state must be [B, Hv, Dv, Dk]", op));
-  if (qa->dtype != ka->dtype || qa->dtype != va->dtype || (qa->dtype != QMM_BFLOAT16 && qa->dtype != QMM_FLOAT32))
-    return finish(fail("[%s] q, k, v must all be bfloat16 or all float32", op));
-  if (ga->dtype != QMM_FLOAT32 || sa->dtype != QMM_FLOAT32) return finish(fail("[%s] g and state must be float32", op));
-  if (ba->dtype != QMM_BFLOAT16 && ba->dtype != QMM_FLOAT32)
-    return finish(fail("[%s] beta must be bfloat16 or float32", op));
-  if (y_dtype != QMM_BFLOAT16 && y_dtype != QMM_FLOAT32) return finish(fail("[%s] y must be bfloat16 or float32", op));
-  if (Dk != 128 || Dv <= 0 || Dv % 8 != 0 || Hk <= 0 || Hv % Hk != 0)
-    return finish(fail("[%s] needs Dk = 128, Dv a multiple of 8 and Hv a multiple of Hk (got Dk %d, Dv %d, Hk %d, Hv %d)",
-                       op, Dk, Dv, Hk, Hv));
-  if ((((uintptr_t)qa->data) | ((uintptr_t)ka->data) | ((uintptr_t)sa->data)) & 15)
-    return finish(fail("[%s] q, k and state must be 16-byte aligned", op));
+  GdnArgs a;
+  if (gdn_args(op, q, k, v, g, beta, state, y_dtype, &a)) return finish(1);
   hipStream_t st = stream_of(s);
   Arr *ya, *so;
-  if (alloc_arr(y, {B, T, Hv, Dv}, y_dtype, st, &ya)) return finish(1);
-  if (alloc_arr(state_out, {B, Hv, Dv, Dk}, QMM_FLOAT32, st, &so)) return finish(1);
+  if (alloc_arr(y, {a.B, a.T, a.Hv, a.Dv}, y_dtype, st, &ya)) return finish(1);
+  if (alloc_arr(state_out, {a.B, a.Hv, a.Dv, a.Dk}, QMM_FLOAT32, st, &so)) return finish(1);
   if (((uintptr_t)so->data) & 15) return finish(fail("[%s] state_out must be 16-byte aligned", op));
-  if ((int64_t)B * Hv == 0) return finish(0);
-  if (T == 0) {  // no steps: the state passes through
-    hipError_t e = so->data == sa->data ? hipSuccess
-                                        : hipMemcpyAsync(so->data, sa->data, sa->nbytes(), hipMemcpyDeviceToDevice, st);
-    if (e != hipSuccess) return finish(fail_hip(e, op));
-    return finish(0);
-  }
-  GdnArgs a;
-  a.B = B, a.T = T, a.Hk = Hk, a.Hv = Hv, a.Dk = Dk, a.Dv = Dv;
-  a.in_f32 = qa->dtype == QMM_FLOAT32;
-  a.beta_f32 = ba->dtype == QMM_FLOAT32;
-  a.y_f32 = y_dtype == QMM_FLOAT32;
-  a.q = qa->data, a.k = ka->data, a.v = va->data, a.beta = ba->data;
-  a.g = (const float *)ga->data, a.state_in = (const float *)sa->data;
   a.state_out = (float *)so->data, a.y = ya->data;
+  if ((int64_t)a.B * a.Hv == 0) return finish(0);
   hipError_t e;
-  if (gdn_chunked_ok(a)) {  // long T: the chunked form, its per-chunk matrices in a workspace
+  if (a.T == 0) {
+    e = gdn_no_steps(a, st);
+  } else if (gdn_chunked_ok(a)) {  // long T: the chunked form, its per-chunk matrices in a workspace
     void *ws = nullptr;
     if (alloc_device(&ws, gdn_chunked_workspace(a), st)) return finish(1);
     e = launch_gdn_chunked(a, ws, st);
     (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
+  } else {
+    e = launch_gdn(a, st);
+  }
+  if (e != hipSuccess) return finish(fail_hip(e, op));
+  return finish(0);
+}
+
+// The result array *res must already hold exactly this shape and dtype.
+static int preallocated(const char *op, const char *what, qmm_array *res, const std::vector<int> &shape,
+                        qmm_dtype dtype, Arr **out) {
+  Arr *a = res ? (Arr *)res->ctx : nullptr;
+  bool same = a && a->data && a->dtype == dtype && a->ndim == (int)shape.size();
+  for (int i = 0; same && i < a->ndim; ++i) same = a->shape[i] == shape[i];
+  if (!same)
+    return fail("[%s] %s must already hold an array of the result's shape and dtype: this entry point allocates "
+                "nothing", op, what);
+  *out = a;
+  return 0;
+}
+
+int qmm_gdn_recurrence_noalloc(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_array k, qmm_array v,
+                               qmm_array g, qmm_array beta, qmm_array state, qmm_dtype y_dtype, qmm_stream s) {
+  const char *op = "gdn_recurrence_noalloc";
+  if (!y || !state_out) return finish(fail("[%s] null result pointer", op));
+  GdnArgs a;
+  if (gdn_args(op, q, k, v, g, beta, state, y_dtype, &a)) return finish(1);
+  Arr *ya, *so;
+  if (preallocated(op, "*y", y, {a.B, a.T, a.Hv, a.Dv}, y_dtype, &ya)) return finish(1);
+  if (preallocated(op, "*state_out", state_out, {a.B, a.Hv, a.Dv, a.Dk}, QMM_FLOAT32, &so)) return finish(1);
+  if (((uintptr_t)so->data) & 15) return finish(fail("[%s] state_out must be 16-byte aligned", op));
+  a.state_out = (float *)so->data, a.y = ya->data;
+  hipStream_t st = stream_of(s);
+  if ((int64_t)a.B * a.Hv == 0) return finish(0);
+  hipError_t e;
+  if (a.T == 0) {
+    e = gdn_no_steps(a, st);
+  } else if (gdn_chunked_ok(a)) {  // the chunked form, its workspace in the library's static array
+    if (!gdn_noalloc_fits(a)) {
+      GdnArgs one = a;  // one batch, one chunk: the least a launch needs
+      one.B = 1, one.T = 1;
+      return finish(fail("[%s] %d value heads need %zu bytes of workspace per 64-step chunk; the static workspace "
+                         "holds %zu bytes",
+                         op, a.Hv, gdn_chunked_workspace(one), gdn_noalloc_scratch_bytes()));
+    }
+    e = launch_gdn_chunked_noalloc(a, st);
   } else {
     e = launch_gdn(a, st);
   }

@@ -115,6 +115,12 @@ constexpr int GDN_CHUNKED_MIN_T = 96;
 bool gdn_chunked_ok(const GdnArgs &a);
 size_t gdn_chunked_workspace(const GdnArgs &a);
 hipError_t launch_gdn_chunked(const GdnArgs &a, void *workspace, hipStream_t st);
+// The chunked form with its workspace in a static per-GPU array (no allocation): the
+// array's size, whether a call's shape fits it (one batch's value heads x one chunk
+// must), and the launch (several launches when the call's workspace exceeds the array).
+size_t gdn_noalloc_scratch_bytes();
+bool gdn_noalloc_fits(const GdnArgs &a);
+hipError_t launch_gdn_chunked_noalloc(const GdnArgs &a, hipStream_t st);
 
 // Zero-fill `bytes` of device memory.
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st);

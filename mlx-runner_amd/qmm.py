@@ -125,6 +125,8 @@ _SIGS = {
     "qmm_silu_mul": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_stream]),
     "qmm_gdn_recurrence": (c_int, [POINTER(qmm_array), POINTER(qmm_array), qmm_array, qmm_array, qmm_array,
                                    qmm_array, qmm_array, qmm_array, c_int, qmm_stream]),
+    "qmm_gdn_recurrence_noalloc": (c_int, [POINTER(qmm_array), POINTER(qmm_array), qmm_array, qmm_array, qmm_array,
+                                           qmm_array, qmm_array, qmm_array, c_int, qmm_stream]),
     "qmm_mlp_gate_up_silu": (c_int, [POINTER(qmm_array), qmm_array, qmm_array, qmm_array, qmm_array, qmm_array,
                                      qmm_optional_int, qmm_optional_int, c_char_p, qmm_stream]),
     "qmm_mlp_forward_q": (c_int, [POINTER(qmm_array), qmm_weight_map, qmm_array, c_char_p, c_char_p, c_char_p,
@@ -335,6 +337,17 @@ def gdn_recurrence(q: Array, k: Array, v: Array, g: Array, beta: Array, state: A
     check(lib.qmm_gdn_recurrence(byref(yr.h), byref(so.h), q.h, k.h, v.h, g.h, beta.h, state.h, y_dtype, s.h),
           "gdn_recurrence")
     return yr, so
+
+
+def gdn_recurrence_noalloc(q: Array, k: Array, v: Array, g: Array, beta: Array, state: Array, *, y: Array,
+                           state_out: Array, y_dtype: int = BFLOAT16, stream: Stream | None = None):
+    """qmm_gdn_recurrence_noalloc: the recurrence into caller-held results (y and
+    state_out must already be arrays of the result shapes; state_out may be state),
+    allocating nothing: the chunked form's workspace is the library's static array."""
+    s = _stream(stream)
+    check(lib.qmm_gdn_recurrence_noalloc(byref(y.h), byref(state_out.h), q.h, k.h, v.h, g.h, beta.h, state.h,
+                                         y_dtype, s.h), "gdn_recurrence_noalloc")
+    return y, state_out
 
 
 def mlp_gate_up_silu(x: Array, w_gate: Array, s_gate: Array, w_up: Array, s_up: Array, mode: str, *,
