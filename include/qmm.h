@@ -186,6 +186,11 @@ const char *qmm_peek_error_name(void);
 /* Consume the latched message into buf; returns its length, or -1 if none. */
 int qmm_take_error(char *buf, size_t len);
 /* Checkpoints: 0 = no error, QMM_ERR_OOM, QMM_ERR_FAILURE; consume the latch.
+ * An error the HIP runtime holds for the calling thread (hipGetLastError) is
+ * latched first.  They do not wait for the device: an error of work still in
+ * flight surfaces at the call that waits for it (qmm_synchronize,
+ * qmm_array_to_host), which latches it, so call qmm_synchronize before a
+ * checkpoint that must cover all enqueued work.
  * Env QMM_FAULT_CHUNK=<n> / QMM_FAULT_STEP=<n> latch a synthetic memory error at
  * the n-th call of qmm_check_error / qmm_check_error_decode (then disarm). */
 #define QMM_ERR_OOM 1

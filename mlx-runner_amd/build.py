@@ -16,7 +16,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "libqmm.so"
-SOURCES = ["qmv.hip", "qmv_mfma.hip", "gdn.hip", "gdn_chunk.hip", "gemm.hip", "gemm_fp8.hip", "gemm_nvfp4.hip", "quant.hip", "qmm_api.cpp", "weights.cpp"]
+SOURCES = ["qmv.hip", "qmv_mfma.hip", "gdn.hip", "gdn_chunk.hip", "gemm.hip", "gemm_fp8.hip", "gemm_nvfp4.hip", "quant.hip", "qmm_api.cpp", "weights.cpp", "checkpoint.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

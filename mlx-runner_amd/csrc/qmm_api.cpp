@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -92,7 +93,10 @@ int fail(const char *fmt, ...) {
   return 1;
 }
 
+// Latches a failed HIP call's error and clears the runtime's record of it, so that
+// what the runtime still holds at a checkpoint is an error the library has not seen.
 int fail_hip(hipError_t e, const char *what) {
+  (void)hipGetLastError();
   return fail("[%s] %s: %s", what, hipGetErrorName(e), hipGetErrorString(e));
 }
 
@@ -135,7 +139,10 @@ void pool_init() {
   if (g_pool_ready) return;
   g_pool_ready = true;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();  // the op's own allocation reports the problem
+    return;
+  }
   hipMemPool_t pool;
   if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
     uint64_t thr = UINT64_MAX;  // keep freed blocks cached for reuse
@@ -154,6 +161,50 @@ int alloc_device(void **p, size_t bytes, hipStream_t st) {
     (void)hipGetLastError();
     return fail("[qmm::malloc] Unable to allocate %zu bytes: %s (out of memory)", bytes, hipGetErrorName(e));
   }
+  return 0;
+}
+
+// ---------------------------------------------------------------- workspaces
+// One grow-only workspace per (device, stream), for the per-call scratch of the
+// prefill GEMMs and the chunked GDN form.  Calls on one stream are ordered, so they
+// can share it; calls on different streams get different ones.  A buffer the stream
+// outgrows stays allocated until the process ends: a graph captured earlier may
+// still point at it.  Sizes are powers of two from 1 MiB, so what is kept is under
+// twice the largest request.
+namespace {
+std::mutex g_ws_mtx;
+std::map<std::pair<int, uintptr_t>, std::pair<void *, size_t>> g_ws;
+}  // namespace
+
+int workspace(hipStream_t st, size_t bytes, void **out, bool *transient) {
+  *transient = false;
+  *out = nullptr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail_hip(e, "qmm::workspace");
+  std::lock_guard<std::mutex> lk(g_ws_mtx);
+  auto &ent = g_ws[{dev, (uintptr_t)st}];
+  if (ent.first && ent.second >= bytes) {
+    *out = ent.first;
+    return 0;
+  }
+  // While the stream is being captured, growing would record an allocation into the
+  // graph that the cache then keeps: take a transient allocation instead.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    cs = hipStreamCaptureStatusActive;  // unknown: the transient path is safe either way
+  }
+  if (cs != hipStreamCaptureStatusNone) {
+    *transient = true;
+    return alloc_device(out, bytes, st);
+  }
+  size_t cap = (size_t)1 << 20;
+  while (cap < bytes) cap <<= 1;
+  void *p = nullptr;
+  if (alloc_device(&p, cap, st)) return 1;
+  ent = {p, cap};
+  *out = p;
   return 0;
 }
 
@@ -359,11 +410,23 @@ static int consume_latch() {
   return qmm_error_is_memory(buf) ? QMM_ERR_OOM : QMM_ERR_FAILURE;
 }
 
+// An error the HIP runtime holds for the calling thread (a failed call, or a launch or
+// device error a synchronising call reported) joins the latch first.  Nothing here
+// waits for the device: errors of work still in flight surface at the call that waits
+// for it (qmm_synchronize, qmm_array_to_host), which latches them.
+// Without a device the runtime answers every call with hipErrorNoDevice: that is no
+// work's error (an op that needs the device reports it itself).
+static void latch_runtime_error() {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess && e != hipErrorNoDevice) fail_hip(e, "qmm_check_error: pending HIP runtime error");
+}
 int qmm_check_error(void) {
+  latch_runtime_error();
   g_fault_chunk.maybe_fire();
   return consume_latch();
 }
 int qmm_check_error_decode(void) {
+  latch_runtime_error();
   g_fault_step.maybe_fire();
   return consume_latch();
 }
@@ -436,9 +499,18 @@ static int check_wq(const Arr *w, const Arr *sc, int mode, const char *op, int *
   return 0;
 }
 
-// y = x @ deq(W).T for the prepared arguments: picks the kernel family by shape.
-// Returns 0, or non-zero with the error latched.
-static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op) {
+// Workspace bytes run_qmm needs for these arguments (0 for the decode kernels).
+static size_t qmm_workspace(const QmmArgs &a) {
+  if (a.M <= QMV_MAX_M || a.K == 0 || (((uintptr_t)a.x | (uintptr_t)a.w) & 15) != 0) return 0;
+  if (gemm_mxfp8_ok(a)) return gemm_mxfp8_workspace(a);
+  if (gemm_nvfp4_ok(a)) return gemm_nvfp4_workspace(a);
+  return 0;
+}
+
+// y = x @ deq(W).T for the prepared arguments: picks the kernel family by shape.  The
+// prefill GEMMs take their workspace from ws_given (qmm_workspace(a) bytes) or else the
+// stream's.  Returns 0, or non-zero with the error latched.
+static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op, void *ws_given = nullptr) {
   const int K = a.K, N = a.N;
   const bool aligned = (((uintptr_t)a.x | (uintptr_t)a.w) & 15) == 0;
   hipError_t e = hipSuccess;
@@ -449,16 +521,14 @@ static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op) {
       e = launch_qmv_mfma(a, st);
     else
       e = (aligned && qmv_fast_ok(a)) ? launch_qmv(a, st) : launch_qmv_generic(a, st);
-  } else if (aligned && gemm_mxfp8_ok(a)) {
-    void *ws = nullptr;
-    if (alloc_device(&ws, gemm_mxfp8_workspace(a), st)) return 1;
-    e = launch_gemm_mxfp8(a, ws, st);
-    (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
-  } else if (aligned && gemm_nvfp4_ok(a)) {
-    void *ws = nullptr;
-    if (alloc_device(&ws, gemm_nvfp4_workspace(a), st)) return 1;
-    e = launch_gemm_nvfp4(a, ws, st);
-    (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
+  } else if (aligned && (gemm_mxfp8_ok(a) || gemm_nvfp4_ok(a))) {
+    const bool fp8 = gemm_mxfp8_ok(a);
+    const size_t need = fp8 ? gemm_mxfp8_workspace(a) : gemm_nvfp4_workspace(a);
+    void *ws = ws_given;
+    bool transient = false;
+    if (!ws && workspace(st, need, &ws, &transient)) return 1;
+    e = fp8 ? launch_gemm_mxfp8(a, ws, st) : launch_gemm_nvfp4(a, ws, st);
+    if (transient) (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
   } else if (aligned && gemm_ok(a)) {
     e = launch_gemm(a, st);
   } else {
@@ -701,11 +771,12 @@ int qmm_gdn_recurrence(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_arra
   hipError_t e;
   if (a.T == 0) {
     e = gdn_no_steps(a, st);
-  } else if (gdn_chunked_ok(a)) {  // long T: the chunked form, its per-chunk matrices in a workspace
+  } else if (gdn_chunked_ok(a)) {  // long T: the chunked form, its per-chunk matrices in the stream's workspace
     void *ws = nullptr;
-    if (alloc_device(&ws, gdn_chunked_workspace(a), st)) return finish(1);
+    bool transient = false;
+    if (workspace(st, gdn_chunked_workspace(a), &ws, &transient)) return finish(1);
     e = launch_gdn_chunked(a, ws, st);
-    (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
+    if (transient) (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
   } else {
     e = launch_gdn(a, st);
   }
@@ -809,30 +880,26 @@ int qmm_mlp_gate_up_silu(qmm_array *res, qmm_array x, qmm_array w_gate, qmm_arra
     if (e != hipSuccess) return finish(fail_hip(e, op));
     return finish(0);
   }
-  // prefill shapes: the two projections, then the activation
-  const size_t bytes = ha->nbytes();
-  void *g = nullptr, *u = nullptr;
-  if (alloc_device(&g, bytes, st)) return finish(1);
-  if (alloc_device(&u, bytes, st)) {
-    (void)hipFreeAsync(g, st);
-    return finish(1);
-  }
-  int rc = 0;
+  // prefill shapes: the two projections, then the activation; the gate and up results
+  // and the projections' own workspace in the stream's workspace
+  const size_t bytes = (ha->nbytes() + 255) & ~(size_t)255;
+  QmmArgs b = a;
+  b.w = wu;
+  b.s = su;
+  const size_t gemm_ws = std::max(qmm_workspace(a), qmm_workspace(b));
+  void *ws = nullptr;
+  bool transient = false;
+  if (workspace(st, 2 * bytes + gemm_ws, &ws, &transient)) return finish(1);
+  void *g = ws, *u = (char *)ws + bytes, *gws = gemm_ws ? (char *)ws + 2 * bytes : nullptr;
   a.y = g;
-  rc = run_qmm(a, bytes, st, op);
-  if (!rc) {
-    QmmArgs b = a;
-    b.w = wu;
-    b.s = su;
-    b.y = u;
-    rc = run_qmm(b, bytes, st, op);
-  }
+  b.y = u;
+  int rc = run_qmm(a, bytes, st, op, gws);
+  if (!rc) rc = run_qmm(b, bytes, st, op, gws);
   if (!rc) {
     hipError_t e = launch_silu_mul(g, u, ha->data, (int64_t)M * N, a.x_f32, st);
     if (e != hipSuccess) rc = fail_hip(e, op);
   }
-  (void)hipFreeAsync(g, st);
-  (void)hipFreeAsync(u, st);
+  if (transient) (void)hipFreeAsync(ws, st);  // stream-ordered: released after the kernels that use it
   return finish(rc ? 1 : 0);
 }
 

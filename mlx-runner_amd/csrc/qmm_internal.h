@@ -38,6 +38,10 @@ int fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 int fail_hip(hipError_t e, const char *what);
 int finish(int rc);
 int alloc_device(void **p, size_t bytes, hipStream_t st);
+// Scratch for work enqueued on `st` (at least `bytes`): the stream's grow-only
+// workspace, or while the stream is being captured and that is too small, a
+// transient allocation (*transient) the caller releases after its kernels.
+int workspace(hipStream_t st, size_t bytes, void **out, bool *transient);
 Arr *new_arr(const int *shape, int dim, qmm_dtype dtype);
 int alloc_arr(qmm_array *res, const std::vector<int> &shape, qmm_dtype dtype, hipStream_t st, Arr **out);
 void release_arr(Arr *a);

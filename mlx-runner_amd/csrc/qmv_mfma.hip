@@ -640,6 +640,8 @@ static int qf_cus() {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
       cus = n;
+    else
+      (void)hipGetLastError();  // no device: the caller's launch reports it
   }
   return cus;
 }

@@ -134,3 +134,27 @@ def test_loader_mlp_forward_q(tmp_path, mode, M):
     ref = O.qmm(mode, h, *q["down_proj"])
     ok, fro, worst = O.check_tolerance(O.bf16_bits_to_f32(y), O.bf16_bits_to_f32(ref), **TOL)
     assert ok, (fro, worst)
+
+
+def test_loader_large_tensors_cycle_the_staging_buffers(tmp_path):
+    """A 195.5 MiB packed weight (more than three of the loader's 64 MiB staging chunks,
+    so both staging buffers are refilled after their copies were waited for) at an
+    unaligned data offset, and its scales with an odd byte count, come back
+    byte-identical in HBM (WeightMap.load reads at most 2 GB at a time, AGENTS.md:23)."""
+    rng = np.random.default_rng(77)
+    N, K = 20001, 16 * 1281  # scales: 20001 x 1281 bytes (odd)
+    w = rng.integers(0, 2 ** 32, size=(N, K // 8), dtype=np.uint32)
+    s = rng.integers(0, 256, size=(N, K // 16), dtype=np.uint8)
+    norm = bf16(rng.standard_normal(7))
+    pre = "language_model.model.layers.0."
+    shard = {pre + "input_layernorm.weight": ("BF16", norm), pre + "mlp.down_proj.weight": ("U32", w),
+             pre + "mlp.down_proj.scales": ("U8", s)}
+    write_safetensors(tmp_path / "model-00001-of-00001.safetensors", shard)
+    (tmp_path / "model.safetensors.index.json").write_text(
+        json.dumps({"weight_map": {k: "model-00001-of-00001.safetensors" for k in shard}}))
+    assert w.nbytes > 3 * (64 << 20) and s.nbytes % 2 == 1
+    wmap = Q.WeightMap(str(tmp_path))
+    assert wmap.quant == ("nvfp4", 16, 4)
+    assert np.array_equal(wmap.get(pre + "mlp.down_proj.weight").numpy(), w)
+    assert np.array_equal(wmap.get(pre + "mlp.down_proj.scales").numpy(), s)
+    assert np.array_equal(wmap.get(pre + "input_layernorm.weight").numpy(), norm)

@@ -74,3 +74,11 @@ def _hdr(d):
 ])
 def test_infer_quant_spec_rejects_inconsistent_checkpoints(tensors, expect):
     assert Q.infer_quant_spec_json(_hdr(tensors)) == expect
+
+
+@pytest.mark.parametrize("shape", [[-2, -4], [2147483648, 1], [1, 99999999999999999999], [-1]])
+def test_header_rejects_negative_and_oversized_dims(shape):
+    """Dimensions must be non-negative and fit an int (the reference's @intCast of a shape
+    would fail); two negative dimensions must not pass as a positive element count."""
+    h = json.dumps({"w": {"dtype": "U8", "shape": [0], "data_offsets": [0, 8]}}).replace("[0]", json.dumps(shape))
+    assert Q.parse_header_json(h) == "BadHeader"
