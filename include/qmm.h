@@ -134,8 +134,11 @@ int qmm_quantize(qmm_vector_array *res, qmm_array w, qmm_optional_int group_size
  * chunk) and in the state; a negative g gives NaN likewise in the chunked form.
  * From T = 96 (with Dv % 16 == 0) the steps run in chunks of 64 as matrix products
  * (the same recurrence to f32 rounding for g in [0, 1]), with a workspace of
- * B * Hv * ceil(T / 64) * 33 KB allocated on the stream and released after the
- * call's kernels. */
+ * B * Hv * ceil(T / 64) * 33 KB: the library's grow-only workspace of the stream
+ * (one per device and stream, kept until the process ends), or, while the stream
+ * is being captured into a graph and that is too small, an allocation made on the
+ * stream and released after the call's kernels.  The prefill GEMMs of
+ * qmm_quantized_matmul (M > 8) take theirs the same way. */
 int qmm_gdn_recurrence(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_array k, qmm_array v, qmm_array g,
                        qmm_array beta, qmm_array state, qmm_dtype y_dtype, qmm_stream s);
 
