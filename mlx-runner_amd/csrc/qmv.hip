@@ -286,6 +286,9 @@ __global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t
       xr3 = xload(3);
     }
   }
+  // keep every x load ahead of the weight loads (the wait counter counts in issue order: an
+  // x load scheduled after them would make the LDS store below wait for all of them)
+  __builtin_amdgcn_sched_barrier(0);
 
   // 2) weight loads of a segment: clamped addresses, no per-load branches
   auto load_seg = [&](int seg, uint4 (&q)[ISEG][R], uint32_t (&sc)[ISEG][R]) __attribute__((always_inline)) {
@@ -378,14 +381,17 @@ __global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t
   if constexpr (DB) {
     if (nseg > 1) load_seg(1, qb, sb);
   }
+  __builtin_amdgcn_sched_barrier(0);  // the weight loads stay ahead of the x staging barrier
   if constexpr (XLDS) {
     // piece (m, c, j) lands at (m * C + c) * PITCH + 16 j
+    // unconditional: a thread past the last piece loaded that piece (the clamp in xload)
+    // and stores the same bytes to its slot; no branch, so the compiler cannot sink the x
+    // load into one behind the weight loads
     auto xstore = [&](int k, const uint4 &v) __attribute__((always_inline)) {
-      const int p = threadIdx.x + THREADS * k;
-      if (p < pieces) {
-        const int mc = p / L::PIECES, j = p - mc * L::PIECES;
-        *(uint4 *)(xs + mc * L::PITCH + 16 * j) = v;
-      }
+      int p = threadIdx.x + THREADS * k;
+      p = p < pieces ? p : pieces - 1;
+      const int mc = p / L::PIECES, j = p - mc * L::PIECES;
+      *(uint4 *)(xs + mc * L::PITCH + 16 * j) = v;
     };
     xstore(0, xr0);
     xstore(1, xr1);
@@ -393,7 +399,11 @@ __global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t
       xstore(2, xr2);
       xstore(3, xr3);
     }
-    __syncthreads();
+    // a barrier for the LDS stores only: __syncthreads() would also wait for every weight
+    // load in flight (vmcnt(0)), so no chunk could be decoded before the last one landed.
+    // The weight and scale pointers are operands of the asm, so the compiler keeps those
+    // loads ahead of it (it would otherwise sink them past it, to their first use).
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::"s"(w), "s"(w2), "s"(s), "s"(s2) : "memory");
   }
   if constexpr (DB) {
     // two segments in flight: compute one while the next one's loads land
