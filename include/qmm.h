@@ -86,7 +86,10 @@ int qmm_synchronize(qmm_stream s);                /* mlx_synchronize */
  *  mode: "mxfp8" | "nvfp4".  y: [..., M, N] in x's dtype (fp32 accumulation, RNE).
  * If *res already holds an array of exactly the output shape and dtype its
  * buffer is written in place (no allocation); otherwise *res is replaced by a
- * new array. */
+ * new array.  Prefill calls (M > 8) read the scales in a tile-major copy that the
+ * library makes at the first such call with this scales handle (not while the
+ * stream is being captured) and frees with the handle: as with mlx arrays, the
+ * contents behind a handle must not change while it lives. */
 int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array scales, qmm_array biases,
                          bool transpose_w, qmm_optional_int group_size, qmm_optional_int bits,
                          const char *mode, qmm_stream s);

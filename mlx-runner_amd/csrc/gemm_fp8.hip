@@ -496,7 +496,17 @@ bool gemm_mxfp8_ok(const QmmArgs &a) {
 
 size_t gemm_mxfp8_workspace(const QmmArgs &a) {
   const size_t mk = round256(a.M) * a.K, nbk = (size_t)a.K / 32;
-  return 2 * mk + 2 * round256(a.M) * nbk + round256(a.N) * nbk + 256;
+  const bool repack = gemm_mxfp8_pipe_ok(a) && !a.s_tiled;
+  return 2 * mk + 2 * round256(a.M) * nbk + (repack ? round256(a.N) * nbk : 0) + 256;
+}
+
+size_t tiled_scales_bytes(int64_t N, int nb) { return (size_t)round256((size_t)N) * (size_t)nb; }
+
+int gemm_tiled_scale_bytes_per_row(const QmmArgs &a) {
+  if (a.M <= QMV_MAX_M || a.x_f32 || a.K <= 0) return 0;
+  if (gemm_mxfp8_ok(a)) return gemm_mxfp8_pipe_ok(a) && (uintptr_t)a.x % 16 == 0 ? a.K / 32 : 0;
+  if (gemm_nvfp4_ok(a)) return a.K / 16;
+  return 0;
 }
 
 hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
@@ -519,8 +529,12 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
   if (e != hipSuccess) return e;
   const int tiles = ((a.M + F_BM - 1) / F_BM) * ((a.N + F_BN - 1) / F_BN);
   if (pipe) {
-    e = launch_repack_scales(a.s, (int64_t)a.N, a.K / 32, (uint32_t *)swp, st);
-    if (e != hipSuccess) return e;
+    if (a.s_tiled) {
+      swp = (uint8_t *)a.s_tiled;  // already tile-major
+    } else {
+      e = launch_repack_scales(a.s, (int64_t)a.N, a.K / 32, (uint32_t *)swp, st);
+      if (e != hipSuccess) return e;
+    }
     static bool pipe_attr_set = false;
     static int cus = 0;
     if (!pipe_attr_set) {

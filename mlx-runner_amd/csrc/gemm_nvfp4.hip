@@ -241,12 +241,18 @@ bool gemm_nvfp4_ok(const QmmArgs &a) {
          (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.w % 16 == 0 && (uintptr_t)a.s % 4 == 0;
 }
 
-size_t gemm_nvfp4_workspace(const QmmArgs &a) { return round256v(a.N) * (size_t)(a.K / 16) + 256; }
+// Workspace: the scales repacked tile-major, unless they come so (a.s_tiled).
+size_t gemm_nvfp4_workspace(const QmmArgs &a) { return a.s_tiled ? 0 : round256v(a.N) * (size_t)(a.K / 16) + 256; }
 
 hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
   if (!gemm_nvfp4_ok(a)) return hipErrorInvalidValue;
-  hipError_t e = launch_repack_scales(a.s, (int64_t)a.N, a.K / 16, (uint32_t *)ws, st);
-  if (e != hipSuccess) return e;
+  hipError_t e = hipSuccess;
+  const uint8_t *tiled = (const uint8_t *)a.s_tiled;
+  if (!tiled) {
+    e = launch_repack_scales(a.s, (int64_t)a.N, a.K / 16, (uint32_t *)ws, st);
+    if (e != hipSuccess) return e;
+    tiled = (const uint8_t *)ws;
+  }
   static bool attr_set = false;
   if (!attr_set) {
     e = hipFuncSetAttribute((const void *)gemm_nvfp4_pipe_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -256,7 +262,7 @@ hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
   }
   const int tiles = ((a.M + V_BM - 1) / V_BM) * ((a.N + V_BN - 1) / V_BN);
   hipLaunchKernelGGL(gemm_nvfp4_pipe_kernel, dim3(tiles), dim3(V_THREADS), V_LDS, st, (const uint16_t *)a.x, a.w,
-                     (const uint8_t *)ws, (uint16_t *)a.y, a.M, a.N, a.K);
+                     tiled, (uint16_t *)a.y, a.M, a.N, a.K);
   return hipGetLastError();
 }
 

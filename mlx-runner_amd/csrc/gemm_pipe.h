@@ -79,7 +79,6 @@ __global__ __launch_bounds__(256) void repack_scales_kernel(const uint8_t *__res
   }
 }
 
-// Host: launch the repack (16-byte reads when the rows allow it).
-hipError_t launch_repack_scales(const uint8_t *s, int64_t N, int nb, uint32_t *out, hipStream_t st);
+// Host: launch the repack (16-byte reads when the rows allow it); declared in qmm_launch.h.
 
 }  // namespace qmm

@@ -245,6 +245,7 @@ int alloc_arr(qmm_array *res, const std::vector<int> &shape, qmm_dtype dtype, hi
 void release_arr(Arr *a) {
   if (!a) return;
   if (a->owned && a->data) (void)hipFreeAsync(a->data, a->alloc_stream);
+  if (a->tiled) (void)hipFreeAsync(a->tiled, a->tiled_stream);
   delete a;
 }
 
@@ -499,6 +500,40 @@ static int check_wq(const Arr *w, const Arr *sc, int mode, const char *op, int *
   return 0;
 }
 
+// The scales of `sa` in the prefill GEMMs' tile-major layout, made once per handle and kept
+// with it: mlx arrays are immutable, so the contents behind a handle do not change while it
+// lives.  Null when the GEMM for `a` reads the scales as stored, while the stream is being
+// captured and no copy exists yet (it would become part of the graph), or if the copy
+// cannot be made; the GEMM then repacks into its workspace on every call.
+static std::mutex g_tiled_mtx;
+static const uint32_t *tiled_scales(Arr *sa, const QmmArgs &a, hipStream_t st) {
+  const int nb = gemm_tiled_scale_bytes_per_row(a);
+  if (!nb || !sa || sa->ndim != 2 || sa->shape[0] != a.N || sa->shape[1] != nb) return nullptr;
+  std::lock_guard<std::mutex> lk(g_tiled_mtx);
+  if (sa->tiled && sa->tiled_nb == nb) return (const uint32_t *)sa->tiled;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  pool_init();
+  void *p = nullptr;
+  if (hipMallocAsync(&p, tiled_scales_bytes(a.N, nb), st) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (launch_repack_scales(a.s, (int64_t)a.N, nb, (uint32_t *)p, st) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFreeAsync(p, st);
+    return nullptr;
+  }
+  if (sa->tiled) (void)hipFreeAsync(sa->tiled, sa->tiled_stream);
+  sa->tiled = p;
+  sa->tiled_nb = nb;
+  sa->tiled_stream = st;
+  return (const uint32_t *)p;
+}
+
 // Workspace bytes run_qmm needs for these arguments (0 for the decode kernels).
 static size_t qmm_workspace(const QmmArgs &a) {
   if (a.M <= QMV_MAX_M || a.K == 0 || (((uintptr_t)a.x | (uintptr_t)a.w) & 15) != 0) return 0;
@@ -510,7 +545,8 @@ static size_t qmm_workspace(const QmmArgs &a) {
 // y = x @ deq(W).T for the prepared arguments: picks the kernel family by shape.  The
 // prefill GEMMs take their workspace from ws_given (qmm_workspace(a) bytes) or else the
 // stream's.  Returns 0, or non-zero with the error latched.
-static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op, void *ws_given = nullptr) {
+static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op, void *ws_given = nullptr,
+                   Arr *scales_arr = nullptr) {
   const int K = a.K, N = a.N;
   const bool aligned = (((uintptr_t)a.x | (uintptr_t)a.w) & 15) == 0;
   hipError_t e = hipSuccess;
@@ -523,6 +559,7 @@ static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op, vo
       e = (aligned && qmv_fast_ok(a)) ? launch_qmv(a, st) : launch_qmv_generic(a, st);
   } else if (aligned && (gemm_mxfp8_ok(a) || gemm_nvfp4_ok(a))) {
     const bool fp8 = gemm_mxfp8_ok(a);
+    if (!a.s_tiled) a.s_tiled = tiled_scales(scales_arr, a, st);
     const size_t need = fp8 ? gemm_mxfp8_workspace(a) : gemm_nvfp4_workspace(a);
     void *ws = ws_given;
     bool transient = false;
@@ -586,7 +623,7 @@ int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array sca
   a.w = (const uint8_t *)wa->data;
   a.s = (const uint8_t *)sa->data;
   a.y = ya->data;
-  if (run_qmm(a, ya->nbytes(), st, op)) return finish(1);
+  if (run_qmm(a, ya->nbytes(), st, op, nullptr, sa)) return finish(1);
   return finish(0);
 }
 
@@ -682,7 +719,7 @@ int qmm_quantized_matmul_group(qmm_array *res, size_t n, qmm_array x, const qmm_
     b.w = (const uint8_t *)((Arr *)w[i].ctx)->data;
     b.s = (const uint8_t *)((Arr *)scales[i].ctx)->data;
     b.y = ya[i]->data;
-    if (run_qmm(b, ya[i]->nbytes(), st, op)) return finish(1);
+    if (run_qmm(b, ya[i]->nbytes(), st, op, nullptr, (Arr *)scales[i].ctx)) return finish(1);
   }
   return finish(0);
 }
@@ -886,6 +923,8 @@ int qmm_mlp_gate_up_silu(qmm_array *res, qmm_array x, qmm_array w_gate, qmm_arra
   QmmArgs b = a;
   b.w = wu;
   b.s = su;
+  a.s_tiled = tiled_scales((Arr *)s_gate.ctx, a, st);
+  b.s_tiled = tiled_scales((Arr *)s_up.ctx, b, st);
   const size_t gemm_ws = std::max(qmm_workspace(a), qmm_workspace(b));
   void *ws = nullptr;
   bool transient = false;

@@ -21,6 +21,11 @@ struct Arr {
   int ndim = 0;
   int shape[QMM_MAX_DIM] = {0};
   qmm_dtype dtype = QMM_BOOL;
+  // For a scales array: a copy in the prefill GEMMs' tile-major layout, made at the first
+  // prefill call that reads it and freed with the handle (tiled_nb scale bytes per row).
+  void *tiled = nullptr;
+  int tiled_nb = 0;
+  hipStream_t tiled_stream = nullptr;
   size_t size() const;
   size_t nbytes() const { return size() * dtype_size(dtype); }
 };

@@ -41,6 +41,9 @@ struct QmmArgs {
   const uint8_t *s;  // scale bytes, K/group per row
   void *y;
   const QmmParts *parts = nullptr;  // a grouped call's outputs (then y is unused)
+  // The scales already in the prefill GEMMs' tile-major layout (the repack of
+  // launch_repack_scales), or null: the GEMM then repacks them into its workspace.
+  const uint32_t *s_tiled = nullptr;
 };
 
 // The output descriptor of a call: y as one part, or the grouped call's parts.
@@ -89,6 +92,14 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *workspace, hipStream_t st);
 bool gemm_nvfp4_ok(const QmmArgs &a);
 size_t gemm_nvfp4_workspace(const QmmArgs &a);
 hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *workspace, hipStream_t st);
+
+// The prefill GEMMs' scale layout: for each 256-row tile and each dword d of a row's
+// nb scale bytes, 256 consecutive dwords (one per row).  tiled_scales_bytes(N, nb) bytes.
+size_t tiled_scales_bytes(int64_t N, int nb);
+hipError_t launch_repack_scales(const uint8_t *s, int64_t N, int nb, uint32_t *out, hipStream_t st);
+// Whether the prefill GEMM for these arguments reads tile-major scales (and how many
+// scale bytes per row it repacks): 0 when it reads them as stored.
+int gemm_tiled_scale_bytes_per_row(const QmmArgs &a);
 
 // dequant: out [N, K] float32 (out_f32) or bfloat16.
 hipError_t launch_dequant(int mode, const uint8_t *w, const uint8_t *s, int64_t N, int64_t K, void *out,

@@ -453,3 +453,46 @@ def test_mlp_gate_up_silu_mfma_shapes(mode, M, N):
     ref = O.silu_mul_bf16(O.qmm(mode, xb, wg, sg, cols=cols), O.qmm(mode, xb, wu, su, cols=cols))
     ok, fro, worst = O.check_tolerance(f32(h[:, cols]), f32(ref), **TOL)
     assert ok, (fro, worst)
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+def test_prefill_scales_tiled_copy_kept_with_handle(mode):
+    """Prefill calls read the scales in a tile-major copy the library makes once per scales
+    handle (at its first eager prefill call) and keeps with it.  A call captured into a
+    graph before that copy exists repacks into the stream's workspace inside the graph;
+    replays of that graph, the eager call that makes the copy and later calls that reuse it
+    all give identical bits, within the bar of the oracle."""
+    import torch
+
+    M, N, K = 300, 1000, 1024
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    W = (torch.randn((N, K), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    wq, sc = Q.quantize(Q.Array.from_torch(W), mode)
+    xa = Q.Array.from_torch(x)
+    nan = lambda: torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)  # noqa: E731
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    y_graph = nan()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        Q.quantized_matmul(xa, wq, sc, mode, out=Q.Array.from_torch(y_graph), stream=Q.Stream.torch_current())
+    outs = []
+    for _ in range(2):
+        y_graph.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        outs.append(y_graph.clone())
+    for _ in range(3):  # the first makes the tile-major copy, the others reuse it
+        y = nan()
+        Q.quantized_matmul(xa, wq, sc, mode, out=Q.Array.from_torch(y))
+        outs.append(y)
+    torch.cuda.synchronize()
+    for y in outs:
+        assert torch.isfinite(y.float()).all()
+        assert torch.equal(y.view(torch.int16), outs[0].view(torch.int16))
+    ref = O.qmm(mode, x.view(torch.int16).cpu().numpy().view(np.uint16), wq.numpy(), sc.numpy())
+    ok, fro, worst = O.check_tolerance(f32(outs[-1].view(torch.int16).cpu().numpy().view(np.uint16)), f32(ref), **TOL)
+    assert ok, (fro, worst)
