@@ -136,6 +136,13 @@ __device__ __forceinline__ void qf_write_records(uint8_t *tile, const uint4 (&xi
   if (lane < 4 * M) *(uint4 *)(tile + lane * QF_REC + 256) = make_uint4(0, 0, 0, 0);
 }
 
+// First row of workgroup b when N rows are spread over the grid: the first rrem
+// workgroups take rbase + 1 rows, the others rbase (rbase = N / grid and rrem =
+// N % grid, from the host).  A division here would cost every wave ~150 scalar
+// instructions and a second kernel-argument round trip before its first load
+// (measured: the first weight load issued 0.9 us after the wave started).
+__device__ __forceinline__ int rows_begin(int b, int rbase, int rrem) { return b * rbase + (b < rrem ? b : rrem); }
+
 // A unit is one wave's K slice (512 elements = 4 chunks of 128) of one 16-row block:
 //   nvfp4: 16 rows x 256 bytes = 4 loads of 1 KiB (4 rows x 256 contiguous bytes each)
 //   mxfp8: 16 rows x 512 bytes = 8 loads of 1 KiB (2 rows x 512 contiguous bytes each)
@@ -177,15 +184,15 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__rest
                                                           const uint8_t *__restrict__ w,
                                                           const uint8_t *__restrict__ s, const uint8_t *__restrict__ w2,
                                                           const uint8_t *__restrict__ s2, const YOut yo,
-                                                          int N, int K, int F) {
+                                                          int N, int K, int F, int rbase, int rrem) {
   using G = QfGeom<MODE>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
   uint8_t *tile = lds + q * G::WAVE_LDS;
   float *part = (float *)(lds + Q * G::WAVE_LDS);  // [F][M][Q][16] partial sums
   constexpr int RB = NMAT == 2 ? 8 : 16;            // output rows per unit
-  const int r_begin = (int)((int64_t)N * blockIdx.x / gridDim.x);
-  const int r_end = (int)((int64_t)N * (blockIdx.x + 1) / gridDim.x);
+  const int r_begin = rows_begin(blockIdx.x, rbase, rrem);
+  const int r_end = rows_begin(blockIdx.x + 1, rbase, rrem);
   const int nrb = (r_end - r_begin + RB - 1) / RB;
   const int S = K >> 9;  // 512-element slices
   auto slice_of = [&](int p) __attribute__((always_inline)) {
@@ -455,14 +462,14 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__re
                                                             const uint8_t *__restrict__ s,
                                                             const uint8_t *__restrict__ w2,
                                                             const uint8_t *__restrict__ s2, const YOut yo,
-                                                            int N, int K, int F) {
+                                                            int N, int K, int F, int rbase, int rrem) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
   uint8_t *tile = lds + q * Q32_WAVE_LDS;
   float *part = (float *)(lds + Q * Q32_WAVE_LDS);  // [F][M][Q][2][32] partial sums (wave, lane half)
   constexpr int RB = NMAT == 2 ? 16 : 32;            // output rows per unit
-  const int r_begin = (int)((int64_t)N * blockIdx.x / gridDim.x);
-  const int r_end = (int)((int64_t)N * (blockIdx.x + 1) / gridDim.x);
+  const int r_begin = rows_begin(blockIdx.x, rbase, rrem);
+  const int r_end = rows_begin(blockIdx.x + 1, rbase, rrem);
   const int nrb = (r_end - r_begin + RB - 1) / RB;
   const int S = K >> 9;
   auto slice_of = [&](int p) __attribute__((always_inline)) {
@@ -715,7 +722,7 @@ static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *
     attr_set = true;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), lds, st, (const uint16_t *)a.x, a.w, a.s, w2, s2,
-                     yout_of(a), a.N, a.K, F);
+                     yout_of(a), a.N, a.K, F, a.N / grid, a.N % grid);
   return hipGetLastError();
 }
 
@@ -772,7 +779,7 @@ static hipError_t launch_q32(const QmmArgs &a, const uint8_t *w2, const uint8_t 
     attr_set = true;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), q32_lds_bytes(M, Q, F), st, (const uint16_t *)a.x, a.w, a.s, w2,
-                     s2, yout_of(a), a.N, a.K, F);
+                     s2, yout_of(a), a.N, a.K, F, a.N / grid, a.N % grid);
   return hipGetLastError();
 }
 
