@@ -236,21 +236,22 @@ constexpr size_t QMV_LDS_MAX = 64 * 1024;
 
 // MLP: the wave's two rows are row n of W (gate) and row n of W2 (up), and the
 // output is silu(gate) * up with the reference's bf16 roundings (silu_mul_bf16).
-template <int MODE, int M, int R, int ISEG, int XP, bool DB, bool MLP = false, bool PARTS = false>
-__global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t *__restrict__ x,
+// WV: waves per workgroup (QMV_WAVES, or 5 where that spreads the rows evenly over the CUs).
+template <int MODE, int M, int R, int ISEG, int XP, bool DB, bool MLP = false, bool PARTS = false, int WV = QMV_WAVES>
+__global__ __launch_bounds__(64 * WV) void qmv_bf16_kernel(const uint16_t *__restrict__ x,
                                                                   const uint8_t *__restrict__ w,
                                                                   const uint8_t *__restrict__ s,
                                                                   const YOut yo, int N, int K,
                                                                   const uint8_t *__restrict__ w2 = nullptr,
                                                                   const uint8_t *__restrict__ s2 = nullptr) {
   using L = XLayout<MODE>;
-  constexpr int THREADS = 64 * QMV_WAVES;
+  constexpr int THREADS = 64 * WV;
   constexpr bool XLDS = XP > 0;  // XP: x pieces staged per thread (2 or 4; 0: x read from global)
   static_assert(XP == 0 || XP == 2 || XP == 4, "x staging supports 2 or 4 pieces per thread");
   static_assert(!MLP || R == 2, "the MLP form pairs one gate row with one up row");
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n0 = (blockIdx.x * QMV_WAVES + wave) * (MLP ? 1 : R);
+  const int n0 = (blockIdx.x * WV + wave) * (MLP ? 1 : R);
   const int64_t row_bytes = (MODE == MXFP8) ? (int64_t)K : (int64_t)(K >> 1);
   const int C = (int)(row_bytes >> 4);
   const int spr = (MODE == MXFP8) ? (K >> 5) : (K >> 4);
@@ -452,25 +453,52 @@ __global__ __launch_bounds__(64 * QMV_WAVES) void qmv_bf16_kernel(const uint16_t
   }
 }
 
-template <int MODE, int M, int R, int ISEG, bool DB, bool PARTS = false>
+template <int MODE, int M, int R, int ISEG, bool DB, bool PARTS = false, int WV = QMV_WAVES>
 static hipError_t launch_qmv_bf16_t(const QmmArgs &a, hipStream_t st) {
   const size_t lds = qmv_lds_bytes(MODE, M, a.K);
   const int C = MODE == MXFP8 ? a.K / 16 : a.K / 32;
   const int pieces = M * C * (MODE == NVFP4 ? 4 : 2);
-  constexpr int T = 64 * QMV_WAVES;
-  dim3 grid((a.N + R * QMV_WAVES - 1) / (R * QMV_WAVES));
+  constexpr int T = 64 * WV;
+  dim3 grid((a.N + R * WV - 1) / (R * WV));
   const uint16_t *x = (const uint16_t *)a.x;
   const YOut y = yout_of(a);
   if (lds <= QMV_LDS_MAX && pieces <= 2 * T)
-    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 2, DB, false, PARTS>), grid, dim3(T), lds, st, x, a.w, a.s,
-                       y, a.N, a.K);
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 2, DB, false, PARTS, WV>), grid, dim3(T), lds, st, x, a.w,
+                       a.s, y, a.N, a.K);
   else if (lds <= QMV_LDS_MAX && pieces <= 4 * T)
-    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 4, DB, false, PARTS>), grid, dim3(T), lds, st, x, a.w, a.s,
-                       y, a.N, a.K);
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 4, DB, false, PARTS, WV>), grid, dim3(T), lds, st, x, a.w,
+                       a.s, y, a.N, a.K);
   else
-    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 0, DB, false, PARTS>), grid, dim3(T), 0, st, x, a.w, a.s,
-                       y, a.N, a.K);
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 0, DB, false, PARTS, WV>), grid, dim3(T), 0, st, x, a.w,
+                       a.s, y, a.N, a.K);
   return hipGetLastError();
+}
+
+// Whether 5-wave workgroups spread N rows (one per wave) over the CUs more evenly
+// than 8-wave ones.  A CU takes whole workgroups, and the time is set by the CUs
+// with the most rows: N = 5120 in 640 8-wave workgroups leaves half the CUs three
+// (24 rows) and half two, in 1024 5-wave ones every CU gets four (20 rows).
+// Measured at mxfp8 N = K = 5120 (one box, per-wave timestamps): 6.91 -> 6.57 us;
+// 10-wave workgroups (two per CU) gained nothing and 4-wave ones slightly less.
+static int qmv_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      cus = n;
+    else
+      (void)hipGetLastError();  // no device: the caller's launch reports it
+  }
+  return cus;
+}
+static bool qmv_five_waves(int N) {
+  const int cus = qmv_cus();
+  if (cus <= 0) return false;
+  auto max_rows = [&](int wv) {  // rows of the most loaded CU
+    const int64_t grid = (N + (int64_t)wv - 1) / wv;
+    return (grid + cus - 1) / cus * (int64_t)wv;
+  };
+  return max_rows(5) < max_rows(QMV_WAVES);
 }
 
 // Rows per wave: two where the grid stays large (the gate+up shape, N = 34816:
@@ -482,6 +510,10 @@ template <int MODE, int M, bool PARTS>
 static hipError_t launch_qmv_bf16_p(const QmmArgs &a, hipStream_t st) {
   const int C = MODE == MXFP8 ? a.K / 16 : a.K / 32;
   if (M == 1 && a.N < 16384) {
+    if (qmv_five_waves(a.N)) {
+      if (C <= 3 * 64) return launch_qmv_bf16_t<MODE, M, 1, 3, false, PARTS, 5>(a, st);
+      return launch_qmv_bf16_t<MODE, M, 1, 5, false, PARTS, 5>(a, st);
+    }
     if (C <= 3 * 64) return launch_qmv_bf16_t<MODE, M, 1, 3, false, PARTS>(a, st);
     return launch_qmv_bf16_t<MODE, M, 1, 5, false, PARTS>(a, st);
   }
