@@ -453,18 +453,13 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
   if (grp == 0) pp_run(std::integral_constant<int, 0>{});
   else pp_run(std::integral_constant<int, 1>{});
 
-  // epilogue: 32x32 accumulator element v of lane l is row 8 (v / 4) + 4 (l / 32) + v % 4, col l % 32
-#pragma unroll
-  for (int i = 0; i < G::FI; ++i)
-#pragma unroll
-    for (int j = 0; j < G::FJ; ++j) {
-      const int col = n0 + wn * (TS / 2) + j * 32 + (lane & 31);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * (TS / 4) + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (row < M && col < n_end) y[(int64_t)row * N + col] = f32_to_bf16_rne(acc[i][j][v]);
-      }
-    }
+  // epilogue through LDS (the ring is idle: every wave has passed the last barrier,
+  // after which no fragment read or DMA is outstanding); wave w's region follows w - 1's
+  constexpr int REGION = 32 * G::FI * (64 * G::FJ + 32);
+  static_assert(8 * REGION <= G::LDS, "the epilogue regions fit the ring");
+  const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
+  gp_store_tile_bf16<G::FI, G::FJ, 0, G::FI>(acc, lds + wave * REGION, lane, y, M, N, m0 + wm * (TS / 4),
+                                             n0 + wn * (TS / 2), n_end, vec);
 }
 
 // K % 128: whole step pairs (the tile-major scale layout); W rows must be 16-byte

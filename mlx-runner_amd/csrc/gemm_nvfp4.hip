@@ -218,18 +218,15 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
   if (grp == 0) pp_run(std::integral_constant<int, 0>{});
   else pp_run(std::integral_constant<int, 1>{});
 
-  // epilogue: 32x32 accumulator element v of lane l is row 8 (v / 4) + 4 (l / 32) + v % 4, col l % 32
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * 128 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (row < M && col < N) y[(int64_t)row * N + col] = f32_to_bf16_rne(acc[i][j][v]);
-      }
-    }
+  // epilogue through LDS (the ring is idle: every wave has passed the last barrier, after
+  // which no fragment read or DMA is outstanding), in two halves of the wave's 128 rows
+  // so that the eight regions fit the ring
+  constexpr int REGION = 64 * (64 * 2 + 32);
+  static_assert(8 * REGION <= V_LDS, "the epilogue regions fit the ring");
+  const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
+  uint8_t *region = lds + wave * REGION;
+  gp_store_tile_bf16<4, 2, 0, 2>(acc, region, lane, y, M, N, m0 + wm * 128, n0 + wn * 64, N, vec);
+  gp_store_tile_bf16<4, 2, 2, 2>(acc, region, lane, y, M, N, m0 + wm * 128, n0 + wn * 64, N, vec);
 }
 
 static size_t round256v(size_t v) { return (v + 255) & ~(size_t)255; }
