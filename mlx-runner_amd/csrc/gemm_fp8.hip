@@ -50,34 +50,10 @@ __host__ __device__ __forceinline__ int64_t packed_scale_index(int64_t r, int b,
 // scales sh, sl from ceil_scale_exp, so no element is clamped.  The rounding is
 // v_cvt_pk_fp8_f32 (OCP E4M3, nearest-even; measured identical to a software
 // nearest-even on every input this pass produces); x - hi * 2^sh is exact in f32.
-template <bool PACKED>
-__global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict__ x, uint32_t total, int rows, int K,
-                                                      uint8_t *__restrict__ xh, uint8_t *__restrict__ xl,
-                                                      uint8_t *__restrict__ sh, uint8_t *__restrict__ sl) {
-  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-  // lanes past the end (the grid is whole blocks) compute on a clamped index and
-  // store nothing; total is even, so the two lanes of a block are both live or not
-  const bool live = i < total;
-  const uint32_t ii = live ? i : total - 1;
-  const uint32_t L = (uint32_t)K >> 4;  // threads per row
-  uint32_t r, c;
-  if (PACKED) {
-    // a wave takes 16 rows x one 64-element K step: lane l -> row l / 4, 16
-    // elements l % 4 of the step, so a row's 64 output bytes (one slot row of
-    // the step's block) come from 4 adjacent lanes and the wave writes 1 KiB
-    // of consecutive slots; the reads are 16 whole 128-byte row pieces
-    const uint32_t S = (uint32_t)K >> 6, w = ii >> 6, l = ii & 63;
-    const uint32_t rg = w / S, st = w - rg * S;
-    r = 16 * rg + (l >> 2);
-    c = 4 * st + (l & 3);
-  } else {
-    r = ii / L;
-    c = ii - r * L;
-  }
-  const int b = (int)(c >> 1), j = (int)(c & 1);
-  const uint32_t rl = (int)r < rows ? r : (uint32_t)rows - 1;  // padded rows (packed) read the last row
-  const uint4 *src = (const uint4 *)(x + (int64_t)rl * K + 16 * c);
-  const uint4 q0 = src[0], q1 = src[1];
+// The split of 16 consecutive elements (lane pair l, l ^ 1 shares a 32-block): E4M3
+// hi / lo words and the block's exponents th, tl.
+__device__ __forceinline__ void split16(const uint4 q0, const uint4 q1, uint32_t (&hw)[4], uint32_t (&lw)[4], int &th,
+                                        int &tl) {
   const uint32_t w8[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
   float v[16];
   float amax = 0.f;
@@ -89,8 +65,7 @@ __global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict
 #pragma unroll
   for (int t = 0; t < 16; ++t) amax = fmaxf(amax, fabsf(v[t]));
   amax = fmaxf(amax, __shfl_xor(amax, 1));
-  const int th = amax > 0.f ? ceil_scale_exp(amax) : -127;
-  uint32_t hw[4], lw[4];
+  th = amax > 0.f ? ceil_scale_exp(amax) : -127;
   float rmax = 0.f;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -108,7 +83,7 @@ __global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict
     for (int u = 0; u < 4; ++u) rmax = fmaxf(rmax, fabsf(v[4 * t + u]));
   }
   rmax = fmaxf(rmax, __shfl_xor(rmax, 1));
-  const int tl = rmax > 0.f ? ceil_scale_exp(rmax) : -127;
+  tl = rmax > 0.f ? ceil_scale_exp(rmax) : -127;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     int cv = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t], -tl), __builtin_ldexpf(v[4 * t + 1], -tl), 0,
@@ -117,21 +92,78 @@ __global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict
                                          true);
     lw[t] = (uint32_t)cv;
   }
-  if (!live || (PACKED && r >= rows)) return;
-  int64_t o;  // byte offset of this lane's 16 bytes
-  if (PACKED) {
-    const int64_t blk = ((int64_t)(r >> 8) * (K >> 6) + (b >> 1)) * 16384;
-    const int rr = (int)(r & 255), part = 2 * (b & 1) + j;
-    o = blk + 16 * (4 * rr + (part ^ p_swz(rr)));
-  } else {
-    o = (int64_t)r * K + 16 * c;
-  }
+}
+
+// Row-major form: one thread per (row, 16 elements).
+__global__ __launch_bounds__(256) void split_x_kernel(const uint16_t *__restrict__ x, uint32_t total, int rows, int K,
+                                                      uint8_t *__restrict__ xh, uint8_t *__restrict__ xl,
+                                                      uint8_t *__restrict__ sh, uint8_t *__restrict__ sl) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  // lanes past the end (the grid is whole blocks) compute on a clamped index and
+  // store nothing; total is even, so the two lanes of a block are both live or not
+  const bool live = i < total;
+  const uint32_t ii = live ? i : total - 1;
+  const uint32_t L = (uint32_t)K >> 4;  // threads per row
+  const uint32_t r = ii / L, c = ii - r * L;
+  const int b = (int)(c >> 1), j = (int)(c & 1);
+  const uint4 *src = (const uint4 *)(x + (int64_t)r * K + 16 * c);
+  uint32_t hw[4], lw[4];
+  int th, tl;
+  split16(src[0], src[1], hw, lw, th, tl);
+  if (!live) return;
+  const int64_t o = (int64_t)r * K + 16 * c;
   *(uint4 *)(xh + o) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
   *(uint4 *)(xl + o) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
   if (j == 0) {
-    const int64_t so = PACKED ? packed_scale_index(r, b, K) : (int64_t)r * (K >> 5) + b;
-    sh[so] = (uint8_t)(th + 127);
-    sl[so] = (uint8_t)(tl + 127);
+    sh[(int64_t)r * (K >> 5) + b] = (uint8_t)(th + 127);
+    sl[(int64_t)r * (K >> 5) + b] = (uint8_t)(tl + 127);
+  }
+}
+
+// Pre-tiled form for the pipelined GEMM: a wave takes 16 rows x U consecutive 64-wide K
+// steps; in each step lane l takes row l / 4, 16 elements l % 4 of the step, so a row's
+// 64 output bytes (one slot row of the step's block) come from 4 adjacent lanes and the
+// wave writes 1 KiB of consecutive slots.  All U steps' reads (16 whole 128-byte row
+// pieces each) are issued before the first is split, so a wave has U x 2 KiB in flight.
+// total = waves x 64 threads, waves = rows16 / 16 x S / U with S = K / 64 (S % U == 0);
+// rows past `rows` (up to the 16-row group) read the last row and store nothing.
+template <int U>
+__global__ __launch_bounds__(256) void split_x_packed_kernel(const uint16_t *__restrict__ x, uint32_t total, int rows,
+                                                             int K, uint8_t *__restrict__ xh, uint8_t *__restrict__ xl,
+                                                             uint8_t *__restrict__ sh, uint8_t *__restrict__ sl) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  const bool live = i < total;  // whole waves: a wave is all live or all not
+  const uint32_t ii = live ? i : total - 1;
+  const uint32_t SU = ((uint32_t)K >> 6) / U, w = ii >> 6, l = ii & 63;
+  const uint32_t rg = w / SU, st0 = U * (w - rg * SU);
+  const uint32_t r = 16 * rg + (l >> 2);
+  const uint32_t rl = (int)r < rows ? r : (uint32_t)rows - 1;
+  uint4 q[U][2];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint4 *src = (const uint4 *)(x + (int64_t)rl * K + 16 * (4 * (st0 + u) + (l & 3)));
+    q[u][0] = src[0];
+    q[u][1] = src[1];
+  }
+  const int rr = (int)(r & 255);
+  const int64_t tile = (int64_t)(r >> 8) * (K >> 6);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    uint32_t hw[4], lw[4];
+    int th, tl;
+    split16(q[u][0], q[u][1], hw, lw, th, tl);
+    const uint32_t c = 4 * (st0 + u) + (l & 3);
+    const int b = (int)(c >> 1), j = (int)(c & 1);
+    if (live && (int)r < rows) {
+      const int64_t o = (tile + (b >> 1)) * 16384 + 16 * (4 * rr + ((2 * (b & 1) + j) ^ p_swz(rr)));
+      *(uint4 *)(xh + o) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      *(uint4 *)(xl + o) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+      if (j == 0) {
+        const int64_t so = packed_scale_index(r, b, K);
+        sh[so] = (uint8_t)(th + 127);
+        sl[so] = (uint8_t)(tl + 127);
+      }
+    }
   }
 }
 
@@ -510,16 +542,22 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
   uint8_t *xh = (uint8_t *)ws, *xl = xh + mk, *sh = xl + mk, *sl = sh + round256(a.M) * nbk;
   uint8_t *swp = sl + round256(a.M) * nbk;
   const bool pipe = gemm_mxfp8_pipe_ok(a);
-  // one thread per (row, 16 elements); the packed form covers rows in groups of 16
-  const int64_t total = (pipe ? ((int64_t)a.M + 15) / 16 * 16 : (int64_t)a.M) * (a.K / 16);
-  if (total >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+  // one thread per (row, 16 elements); the packed form covers rows in groups of 16 and
+  // U steps per thread (4 when K % 256 == 0, else 2: K % 128 == 0 there)
+  const int64_t rows_t = pipe ? ((int64_t)a.M + 15) / 16 * 16 : (int64_t)a.M;
+  const int U = pipe && a.K % 256 == 0 ? 4 : 2;
+  const int64_t total = rows_t * (a.K / 16) / (pipe ? U : 1);
+  if (rows_t * (a.K / 16) >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   const unsigned sb = (unsigned)((total + 255) / 256);
-  if (pipe)
-    hipLaunchKernelGGL(split_x_kernel<true>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (uint32_t)total, a.M,
-                       a.K, xh, xl, sh, sl);
-  else
-    hipLaunchKernelGGL(split_x_kernel<false>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (uint32_t)total,
+  if (pipe && U == 4)
+    hipLaunchKernelGGL(split_x_packed_kernel<4>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (uint32_t)total,
                        a.M, a.K, xh, xl, sh, sl);
+  else if (pipe)
+    hipLaunchKernelGGL(split_x_packed_kernel<2>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (uint32_t)total,
+                       a.M, a.K, xh, xl, sh, sl);
+  else
+    hipLaunchKernelGGL(split_x_kernel, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (uint32_t)total, a.M, a.K,
+                       xh, xl, sh, sl);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int tiles = ((a.M + F_BM - 1) / F_BM) * ((a.N + F_BN - 1) / F_BN);

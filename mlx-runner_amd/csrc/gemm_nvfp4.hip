@@ -46,6 +46,10 @@ constexpr int V_DMA_S = 6, V_DMA = 5;
 }  // namespace
 
 __device__ __forceinline__ int aswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// W tile: row r's two 16-byte halves are stored swapped when wswz(r) = 1, so that the
+// fragment reads of 16 consecutive rows (one half each) fall in distinct banks (rows
+// r and r + 8, and r and r + 4 on 32 banks, would otherwise share them)
+__device__ __forceinline__ int wswz(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
 
 // 8 nvfp4 elements (one dword, lowest nibble first) times the E4M3 scale byte, as 8 bf16.
 __device__ __forceinline__ bf16x8_t deq8_nvfp4(uint32_t word, uint32_t scale_byte) {
@@ -89,8 +93,10 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
     const int q = 64 * g + lane, row = q >> 3, part = (q & 7) ^ aswz(row);
     ga[i] = (const uint8_t *)x + ((int64_t)min(m0 + row, M - 1) * K + part * 8) * 2;
   }
-  // W: wave w moves rows 32 w + lane / 2, bytes 16 (lane % 2) of the step's 32
-  const uint8_t *gw = w + (int64_t)min(n0 + 32 * wave + (lane >> 1), N - 1) * wrow + 16 * (lane & 1);
+  // W: wave w moves rows 32 w + lane / 2, LDS half lane % 2 of the row (the row's half
+  // (lane % 2) ^ wswz(row) of the step's 32 bytes)
+  const int wr = 32 * wave + (lane >> 1);
+  const uint8_t *gw = w + (int64_t)min(n0 + wr, N - 1) * wrow + 16 * ((lane & 1) ^ wswz(wr));
   // scales: wave 0, lane l copies the scale dwords of rows 4 l .. 4 l + 3 (the step's 1 KiB block)
   const uint8_t *gs = sp + ((int64_t)tn * steps * 256 + 4 * lane) * 4;
   const bool sw = wave == 0;
@@ -116,7 +122,7 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int r = wn * 64 + j * 32 + fr;
-    ob[j] = V_ATILE + r * 32 + 16 * fh;
+    ob[j] = V_ATILE + r * 32 + 16 * (fh ^ wswz(r));
     os[j] = V_ATILE + V_WTILE + r * 4;
   }
 

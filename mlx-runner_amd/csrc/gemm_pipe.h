@@ -55,14 +55,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // cols col0 + [0, 32 FJ) of y[M, N]; columns from col_end on are not this call's), bf16
 // out, accumulator blocks i in [I0, I0 + NI).  Element v of lane l of a 32x32 block is
 // row 8 (v / 4) + 4 (l / 32) + v % 4, col l % 32: a store straight from it writes two
-// bytes per lane.  Instead adjacent lanes swap one of each pair of rows (DPP), so each
-// lane holds two adjacent columns of one row, converts them with one packed RNE
+// bytes per lane.  Instead each lane converts its rows 2u, 2u + 1 with one packed RNE
 // conversion (bit-identical to f32_to_bf16_rne on every finite input; a NaN stays a NaN
-// but keeps its sign) and writes the dword to the wave's LDS region; the region is then
-// read back 16 bytes per lane along rows, so every global store writes 16 contiguous
-// bytes (vec: N % 8 == 0 and y 16-byte aligned; otherwise, and at the last columns,
-// element stores).  The region, (32 NI) x (64 FJ + 32) bytes, belongs to this wave; the
-// caller guarantees no other wave reads or writes it meanwhile.
+// but keeps its sign), swaps the dword with its neighbour lane (DPP) and keeps one row
+// of the two columns (v_perm: the even lane row 2u, the odd lane row 2u + 1), writes
+// it to the wave's LDS region and reads the region back 16 bytes per lane along rows,
+// so every global store writes 16 contiguous bytes (vec: N % 8 == 0 and y 16-byte
+// aligned; otherwise, and at the last columns, element stores).  The region,
+// (32 NI) x (64 FJ + 32) bytes, belongs to this wave; the caller guarantees that no
+// other wave reads or writes it meanwhile.
 typedef __bf16 gp_bf16x2_t __attribute__((ext_vector_type(2)));
 template <int FI, int FJ, int I0, int NI>
 __device__ __forceinline__ void gp_store_tile_bf16(const f32x16_t (&acc)[FI][FJ], uint8_t *region, int lane,
@@ -71,27 +72,37 @@ __device__ __forceinline__ void gp_store_tile_bf16(const f32x16_t (&acc)[FI][FJ]
   constexpr int PITCH = 64 * FJ + 32;  // bytes per region row (the pad spreads a write's rows over the banks)
   const int c = lane & 31, h = lane >> 5;
   const bool odd = c & 1;
+  // v_perm selector over {neighbour's dword, own dword} (own bytes 0-3, neighbour's 4-7):
+  // even lane: own low half, neighbour's low half (row 2u, columns c, c + 1);
+  // odd lane: neighbour's high half, own high half (row 2u + 1, columns c - 1, c)
+  const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
 #pragma unroll
   for (int i = 0; i < NI; ++i)
 #pragma unroll
     for (int j = 0; j < FJ; ++j)
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        // rows 2u and 2u + 1 of the lane's 16: the even lane keeps row 2u (its column and
-        // the odd neighbour's), the odd lane row 2u + 1 (the even neighbour's column and its)
-        const float a0 = acc[I0 + i][j][2 * u], a1 = acc[I0 + i][j][2 * u + 1];
-        const float send = odd ? a0 : a1;
-        const float recv = __builtin_bit_cast(
-            float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, true));  // lane ^ 1
         gp_bf16x2_t w;
-        w[0] = (__bf16)(odd ? recv : a0);
-        w[1] = (__bf16)(odd ? a1 : recv);
+        w[0] = (__bf16)acc[I0 + i][j][2 * u];
+        w[1] = (__bf16)acc[I0 + i][j][2 * u + 1];
+        const uint32_t own = __builtin_bit_cast(uint32_t, w);
+        const uint32_t nb = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0xB1, 0xF, 0xF, true);  // lane ^ 1
+        const uint32_t word = __builtin_amdgcn_perm(nb, own, sel);
         const int row = i * 32 + 8 * (u >> 1) + 4 * h + 2 * (u & 1) + (odd ? 1 : 0);
-        *(uint32_t *)(region + row * PITCH + (j * 32 + (c & ~1)) * 2) = __builtin_bit_cast(uint32_t, w);
+        *(uint32_t *)(region + row * PITCH + (j * 32 + (c & ~1)) * 2) = word;
       }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   constexpr int LPR = FJ * 4;    // lanes per row (16-byte pieces)
   constexpr int RPI = 64 / LPR;  // rows per instruction
+  if (vec && row0 + (I0 + NI) * 32 <= M && col0 + FJ * 32 <= col_end) {  // the whole block is inside
+#pragma unroll
+    for (int it = 0; it < NI * 32 / RPI; ++it) {
+      const int row = it * RPI + lane / LPR, piece = lane % LPR;
+      const uint4 d = *(const uint4 *)(region + row * PITCH + piece * 16);
+      *(uint4 *)(y + (int64_t)(row0 + I0 * 32 + row) * N + col0 + piece * 8) = d;
+    }
+    return;
+  }
 #pragma unroll
   for (int it = 0; it < NI * 32 / RPI; ++it) {
     const int row = it * RPI + lane / LPR, piece = lane % LPR;

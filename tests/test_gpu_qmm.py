@@ -228,7 +228,8 @@ def test_one_hot_x_reads_back_dequantized_rows(mode):
 
 
 @pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
-@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (300, 200, 1024), (129, 96, 5120), (17, 1000, 160)])
+@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (300, 200, 1024), (129, 96, 5120), (17, 1000, 160),
+                                   (40, 200, 384), (33, 130, 1152)])
 def test_prefill_matches_oracle(mode, M, N, K):
     if mode == "mxfp8" and K % 32:
         pytest.skip("mxfp8 needs K % 32 == 0")
