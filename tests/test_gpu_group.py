@@ -79,6 +79,7 @@ GROUPS = {
     "attn_qkv": (12288, 1024, 1024),          # q, k, v
     "ragged_small": (1000, 37, 530, 3),       # part boundaries inside row blocks (bf16 GEMV)
     "ragged_big": (12000, 4099, 301, 77),     # ... and on the MFMA kernels at M = 1
+    "five_wave": (2560, 1280, 1280),          # 5120 rows: the bf16 GEMV's 5-wave workgroups at M = 1
 }
 
 
