@@ -109,6 +109,40 @@ def test_loader_missing_weight_errors(tmp_path):
 
 
 @pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+@pytest.mark.parametrize("M", [1, 2])
+def test_loader_mtp_names(tmp_path, mode, M):
+    """mtpLinearQ (src/mtp.zig:67-70) formats "language_model.mtp.{suffix}" and calls
+    namedLinearQ: the MTP head's fc (K = 2 H, src/mtp.zig:158) and its attention
+    projections (:85-133) load and dispatch under that prefix like the backbone's."""
+    rng = np.random.default_rng(60 + M)
+    H = 512
+    shapes = {"fc": (H, 2 * H), "layers.0.self_attn.q_proj": (96, H), "layers.0.self_attn.o_proj": (H, 64)}
+    q, tensors = {}, {}
+    for name, (n, k) in shapes.items():
+        q[name] = O.quantize(mode, O.bf16_bits_to_f32(bf16(rng.standard_normal((n, k)) * 0.05)))
+        tensors["language_model.mtp." + name + ".weight"] = ("U32", q[name][0])
+        tensors["language_model.mtp." + name + ".scales"] = ("U8", q[name][1])
+    tensors["language_model.mtp.norm.weight"] = ("BF16", bf16(rng.standard_normal(H)))
+    write_safetensors(tmp_path / "model-00001-of-00001.safetensors", tensors)
+    (tmp_path / "model.safetensors.index.json").write_text(
+        json.dumps({"weight_map": {k: "model-00001-of-00001.safetensors" for k in tensors}}))
+    wmap = Q.WeightMap(str(tmp_path))
+    assert wmap.quant == (mode, O.GROUP[mode], O.BITS[mode])
+    for name, (n, k) in shapes.items():
+        xb = bf16(rng.standard_normal((M, k)))
+        y = wmap.named_linear_q(Q.Array.from_numpy(xb, Q.BFLOAT16), "language_model.mtp." + name + ".weight").numpy()
+        assert y.shape == (M, n)
+        ref = O.qmm(mode, xb, *q[name])
+        ok, fro, worst = O.check_tolerance(O.bf16_bits_to_f32(y), O.bf16_bits_to_f32(ref), **TOL)
+        assert ok, (name, fro, worst)
+    x = Q.Array.from_numpy(bf16(np.ones((1, H))), Q.BFLOAT16)
+    with pytest.raises(Q.QmmError, match="MissingWeight"):
+        wmap.named_linear_q(x, "language_model.mtp.layers.0.self_attn.k_proj.weight")  # absent
+    with pytest.raises(Q.QmmError, match="MissingWeight"):
+        wmap.named_linear_q(x, "mtp.fc.weight")  # without the language_model. prefix
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
 @pytest.mark.parametrize("M", [1, 20])
 def test_loader_mlp_forward_q(tmp_path, mode, M):
     """mlpForwardQ (src/model.zig:905-915): down(silu(gate(x)) * up(x)) by names,
