@@ -173,13 +173,14 @@ def test_decode_long_k_matches_oracle(mode, M, N, K):
     assert np.array_equal(run_qmm(mode, xb, wq, s), y)
 
 
-@pytest.mark.parametrize("K", [256, 384])
+@pytest.mark.parametrize("K", [128, 256, 384, 512])
 def test_prefill_mxfp8_partial_last_round(K):
     """x rows 300 (ragged against the 256-row tiles), W rows 33180: on a 256-CU
     part the 256 x 256 tiles leave a last round of 4 tiles, which runs as 128 x 128
     tiles over the last two tile-columns; every column from there on is checked
-    (plus a sample of the rest), all rows, at K = 256 (two step pairs) and 384
-    (three), and a second call must return the same bits."""
+    (plus a sample of the rest), all rows, at K = 128 to 512 (the tail kernel's
+    2-step, 4-step, 6-step and looped 8-step schedules), and a second call must
+    return the same bits."""
     mode, M, N = "mxfp8", 300, 33180
     rng = np.random.default_rng(11)
     wq, s = rand_w(rng, mode, N, K)
