@@ -66,31 +66,34 @@ __device__ __forceinline__ void split16(const uint4 q0, const uint4 q1, uint32_t
   for (int t = 0; t < 16; ++t) amax = fmaxf(amax, fabsf(v[t]));
   amax = fmaxf(amax, __shfl_xor(amax, 1));
   th = amax > 0.f ? ceil_scale_exp(amax) : -127;
+  // hi straight from the bf16 pairs (the conversion divides by 2^th and rounds to nearest
+  // even), then back to f32 times 2^th for the residual, which is exact in f32
+  const float sh = e8m0_scale_operand(th);
   float rmax = 0.f;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    int cv = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t], -th), __builtin_ldexpf(v[4 * t + 1], -th), 0,
-                                             false);
-    cv = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t + 2], -th), __builtin_ldexpf(v[4 * t + 3], -th), cv,
-                                         true);
-    hw[t] = (uint32_t)cv;
-    const f32x2_t b0 = __builtin_amdgcn_cvt_pk_f32_fp8(cv, false), b1 = __builtin_amdgcn_cvt_pk_f32_fp8(cv, true);
-    v[4 * t] -= __builtin_ldexpf(b0.x, th);
-    v[4 * t + 1] -= __builtin_ldexpf(b0.y, th);
-    v[4 * t + 2] -= __builtin_ldexpf(b1.x, th);
-    v[4 * t + 3] -= __builtin_ldexpf(b1.y, th);
+    i16x2_t c = {0, 0};
+    c = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c, __builtin_bit_cast(bf16x2_t, w8[2 * t]), sh, false);
+    c = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c, __builtin_bit_cast(bf16x2_t, w8[2 * t + 1]), sh, true);
+    hw[t] = __builtin_bit_cast(uint32_t, c);
+    const f32x2_t b0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hw[t], sh, false);
+    const f32x2_t b1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hw[t], sh, true);
+    v[4 * t] -= b0.x;
+    v[4 * t + 1] -= b0.y;
+    v[4 * t + 2] -= b1.x;
+    v[4 * t + 3] -= b1.y;
 #pragma unroll
     for (int u = 0; u < 4; ++u) rmax = fmaxf(rmax, fabsf(v[4 * t + u]));
   }
   rmax = fmaxf(rmax, __shfl_xor(rmax, 1));
   tl = rmax > 0.f ? ceil_scale_exp(rmax) : -127;
+  const float sl = e8m0_scale_operand(tl);
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    int cv = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t], -tl), __builtin_ldexpf(v[4 * t + 1], -tl), 0,
-                                             false);
-    cv = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(v[4 * t + 2], -tl), __builtin_ldexpf(v[4 * t + 3], -tl), cv,
-                                         true);
-    lw[t] = (uint32_t)cv;
+    i16x2_t c = {0, 0};
+    c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(c, v[4 * t], v[4 * t + 1], sl, false);
+    c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(c, v[4 * t + 2], v[4 * t + 3], sl, true);
+    lw[t] = __builtin_bit_cast(uint32_t, c);
   }
 }
 

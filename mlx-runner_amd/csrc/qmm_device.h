@@ -87,6 +87,15 @@ __device__ __forceinline__ f32x2_t fp8x2_to_f32x2(uint32_t word) {
   return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, HI);
 }
 
+// Scale operand 2^t (t in [-127, 127]) for the v_cvt_scalef32_* conversions, which read
+// only the f32's exponent field as an E8M0 code (field 0, here t = -127, is 2^-127).
+// Measured on gfx950 for every bf16 input at t from -127 to 127:
+//   cvt_scalef32_pk_fp8_f32 / _fp8_bf16 (a, b, 2^t) == cvt_pk_fp8_f32(a * 2^-t, b * 2^-t)
+//   cvt_scalef32_pk_f32_fp8 (w, 2^t)              == cvt_pk_f32_fp8(w) * 2^t
+__device__ __forceinline__ float e8m0_scale_operand(int t) { return __uint_as_float((uint32_t)(t + 127) << 23); }
+
+typedef short i16x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ float dot2_bf16(bf16x2_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(a, __builtin_bit_cast(bf16x2_t, b), c, false);
 }
