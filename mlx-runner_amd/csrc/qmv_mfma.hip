@@ -63,15 +63,12 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 template <int GT>
 __device__ __forceinline__ void split8(const uint4 q, uint2 &hi, uint2 &lo, int &th, int &tl) {
   const uint32_t wv[4] = {q.x, q.y, q.z, q.w};
-  float xf[8], hf[8];
+  float xf[8];
   float amax = 0.f;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     xf[2 * t] = __uint_as_float(wv[t] << 16);
     xf[2 * t + 1] = __uint_as_float(wv[t] & 0xFFFF0000u);
-    const uint32_t hb = wv[t] & 0xFFF0FFF0u;  // sign, exponent, top 3 mantissa bits
-    hf[2 * t] = __uint_as_float(hb << 16);
-    hf[2 * t + 1] = __uint_as_float(hb & 0xFFFF0000u);
   }
 #pragma unroll
   for (int t = 0; t < 8; ++t) amax = fmaxf(amax, fabsf(xf[t]));
@@ -80,19 +77,27 @@ __device__ __forceinline__ void split8(const uint4 q, uint2 &hi, uint2 &lo, int 
   th = amax > 0.f ? ceil_scale_exp(amax) : -127;  // amax * 2^-th <= 448
   // |lo| < 2^(e-3) for an element of exponent e <= e(amax), so lo * 2^-(th-3) < 256
   tl = th - 3 < -127 ? -127 : th - 3;
+  // hi: the bf16 pairs with their mantissas cut to 3 bits (sign, exponent, top 3 bits),
+  // divided by 2^th by the scaled conversion; lo = x - hi in f32 (exact), divided by 2^tl
+  const float sh = e8m0_scale_operand(th), sl = e8m0_scale_operand(tl);
   uint32_t hw[2], lw[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    int c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(hf[4 * t], -th), __builtin_ldexpf(hf[4 * t + 1], -th), 0,
-                                            false);
-    c = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(hf[4 * t + 2], -th), __builtin_ldexpf(hf[4 * t + 3], -th), c,
-                                        true);
-    hw[t] = (uint32_t)c;
-    int d = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(xf[4 * t] - hf[4 * t], -tl),
-                                            __builtin_ldexpf(xf[4 * t + 1] - hf[4 * t + 1], -tl), 0, false);
-    d = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(xf[4 * t + 2] - hf[4 * t + 2], -tl),
-                                        __builtin_ldexpf(xf[4 * t + 3] - hf[4 * t + 3], -tl), d, true);
-    lw[t] = (uint32_t)d;
+    i16x2_t c = {0, 0};
+    c = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c, __builtin_bit_cast(bf16x2_t, wv[2 * t] & 0xFFF0FFF0u), sh, false);
+    c = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c, __builtin_bit_cast(bf16x2_t, wv[2 * t + 1] & 0xFFF0FFF0u), sh,
+                                                  true);
+    hw[t] = __builtin_bit_cast(uint32_t, c);
+    float d[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float x = xf[4 * t + u];
+      d[u] = x - __uint_as_float(__float_as_uint(x) & 0xFFF00000u);
+    }
+    i16x2_t e = {0, 0};
+    e = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(e, d[0], d[1], sl, false);
+    e = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(e, d[2], d[3], sl, true);
+    lw[t] = __builtin_bit_cast(uint32_t, e);
   }
   hi = make_uint2(hw[0], hw[1]);
   lo = make_uint2(lw[0], lw[1]);
