@@ -26,9 +26,15 @@ FLAGS = [
 ]
 
 
+# Decode kernels: the leading kernel arguments (sizes and pointers, 16 dwords) arrive
+# preloaded in SGPRs, so a wave issues its first loads without a kernel-argument round
+# trip (gfx950 firmware; the code keeps a loading prologue for firmware without it).
+EXTRA = {"qmv_mfma.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+
+
 def _compile(src: str) -> Path:
     obj = BUILD / (src + ".o")
-    cmd = [HIPCC, *FLAGS, "-I", str(HERE.parent / "include"), "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-I", str(HERE.parent / "include"), "-c", str(CSRC / src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l)

@@ -185,11 +185,11 @@ constexpr size_t qf_lds_bytes(int M, int Q, int F) {
 // zero), re-splits x for it and adds its partial sums to those of earlier
 // passes; the partials of every row block stay in LDS until the last pass.
 template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false>
-__global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(const uint16_t *__restrict__ x,
+__global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, int rbase, int rrem,
+                                                          const uint16_t *__restrict__ x,
                                                           const uint8_t *__restrict__ w,
                                                           const uint8_t *__restrict__ s, const uint8_t *__restrict__ w2,
-                                                          const uint8_t *__restrict__ s2, const YOut yo,
-                                                          int N, int K, int F, int rbase, int rrem) {
+                                                          const uint8_t *__restrict__ s2, const YOut yo) {
   using G = QfGeom<MODE>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
@@ -462,12 +462,12 @@ constexpr size_t q32_lds_bytes(int M, int Q, int F) { return (size_t)Q * Q32_WAV
 // NMAT = 2: the MLP form, a unit's 32 columns being 16 rows of W (gate) and the
 // same 16 rows of W2 (up); the flush writes silu(gate) * up (as in qmv_mfma_kernel).
 template <int M, int Q, int P, int NMAT, bool PARTS = false>
-__global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(const uint16_t *__restrict__ x,
+__global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F, int rbase, int rrem,
+                                                            const uint16_t *__restrict__ x,
                                                             const uint8_t *__restrict__ w,
                                                             const uint8_t *__restrict__ s,
                                                             const uint8_t *__restrict__ w2,
-                                                            const uint8_t *__restrict__ s2, const YOut yo,
-                                                            int N, int K, int F, int rbase, int rrem) {
+                                                            const uint8_t *__restrict__ s2, const YOut yo) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
   uint8_t *tile = lds + q * Q32_WAVE_LDS;
@@ -726,8 +726,8 @@ static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), lds, st, (const uint16_t *)a.x, a.w, a.s, w2, s2,
-                     yout_of(a), a.N, a.K, F, a.N / grid, a.N % grid);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), lds, st, a.N, a.K, F, a.N / grid, a.N % grid,
+                     (const uint16_t *)a.x, a.w, a.s, w2, s2, yout_of(a));
   return hipGetLastError();
 }
 
@@ -783,8 +783,8 @@ static hipError_t launch_q32(const QmmArgs &a, const uint8_t *w2, const uint8_t 
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), q32_lds_bytes(M, Q, F), st, (const uint16_t *)a.x, a.w, a.s, w2,
-                     s2, yout_of(a), a.N, a.K, F, a.N / grid, a.N % grid);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), q32_lds_bytes(M, Q, F), st, a.N, a.K, F, a.N / grid,
+                     a.N % grid, (const uint16_t *)a.x, a.w, a.s, w2, s2, yout_of(a));
   return hipGetLastError();
 }
 
