@@ -29,7 +29,8 @@ FLAGS = [
 # Decode kernels: the leading kernel arguments (sizes and pointers, 16 dwords) arrive
 # preloaded in SGPRs, so a wave issues its first loads without a kernel-argument round
 # trip (gfx950 firmware; the code keeps a loading prologue for firmware without it).
-EXTRA = {"qmv_mfma.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
+EXTRA = {"qmv_mfma.hip": PRELOAD, "qmv.hip": PRELOAD}
 
 
 def _compile(src: str) -> Path:

@@ -238,12 +238,11 @@ constexpr size_t QMV_LDS_MAX = 64 * 1024;
 // output is silu(gate) * up with the reference's bf16 roundings (silu_mul_bf16).
 // WV: waves per workgroup (QMV_WAVES, or 5 where that spreads the rows evenly over the CUs).
 template <int MODE, int M, int R, int ISEG, int XP, bool DB, bool MLP = false, bool PARTS = false, int WV = QMV_WAVES>
-__global__ __launch_bounds__(64 * WV) void qmv_bf16_kernel(const uint16_t *__restrict__ x,
+__global__ __launch_bounds__(64 * WV) void qmv_bf16_kernel(int N, int K, const uint16_t *__restrict__ x,
                                                                   const uint8_t *__restrict__ w,
                                                                   const uint8_t *__restrict__ s,
-                                                                  const YOut yo, int N, int K,
-                                                                  const uint8_t *__restrict__ w2 = nullptr,
-                                                                  const uint8_t *__restrict__ s2 = nullptr) {
+                                                                  const uint8_t *__restrict__ w2,
+                                                                  const uint8_t *__restrict__ s2, const YOut yo) {
   using L = XLayout<MODE>;
   constexpr int THREADS = 64 * WV;
   constexpr bool XLDS = XP > 0;  // XP: x pieces staged per thread (2 or 4; 0: x read from global)
@@ -463,14 +462,14 @@ static hipError_t launch_qmv_bf16_t(const QmmArgs &a, hipStream_t st) {
   const uint16_t *x = (const uint16_t *)a.x;
   const YOut y = yout_of(a);
   if (lds <= QMV_LDS_MAX && pieces <= 2 * T)
-    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 2, DB, false, PARTS, WV>), grid, dim3(T), lds, st, x, a.w,
-                       a.s, y, a.N, a.K);
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 2, DB, false, PARTS, WV>), grid, dim3(T), lds, st, a.N, a.K,
+                       x, a.w, a.s, nullptr, nullptr, y);
   else if (lds <= QMV_LDS_MAX && pieces <= 4 * T)
-    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 4, DB, false, PARTS, WV>), grid, dim3(T), lds, st, x, a.w,
-                       a.s, y, a.N, a.K);
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 4, DB, false, PARTS, WV>), grid, dim3(T), lds, st, a.N, a.K,
+                       x, a.w, a.s, nullptr, nullptr, y);
   else
-    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 0, DB, false, PARTS, WV>), grid, dim3(T), 0, st, x, a.w,
-                       a.s, y, a.N, a.K);
+    hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, R, ISEG, 0, DB, false, PARTS, WV>), grid, dim3(T), 0, st, a.N, a.K, x,
+                       a.w, a.s, nullptr, nullptr, y);
   return hipGetLastError();
 }
 
@@ -548,8 +547,8 @@ static hipError_t launch_qmv_mlp_m(const QmmArgs &a, const uint8_t *w_up, const 
   const uint16_t *x = (const uint16_t *)a.x;
   const YOut y = yout_of(a);
 #define QMV_MLP_LAUNCH(IS, XP)                                                                                 \
-  hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, 2, IS, XP, false, true>), grid, dim3(T), XP ? lds : 0, st, x, a.w, \
-                     a.s, y, a.N, a.K, w_up, s_up)
+  hipLaunchKernelGGL((qmv_bf16_kernel<MODE, M, 2, IS, XP, false, true>), grid, dim3(T), XP ? lds : 0, st, a.N, a.K, \
+                     x, a.w, a.s, w_up, s_up, y)
   if (C <= 3 * 64) {
     if (lds <= QMV_LDS_MAX && pieces <= 2 * T) QMV_MLP_LAUNCH(3, 2);
     else if (lds <= QMV_LDS_MAX && pieces <= 4 * T) QMV_MLP_LAUNCH(3, 4);
@@ -597,10 +596,9 @@ __device__ __forceinline__ int xswz(int c) {
 constexpr int QLONG_WAVES = 4;
 
 template <int MODE, int M, int ISEG, int R>
-__global__ __launch_bounds__(64 * QLONG_WAVES) void qmv_long_kernel(const uint16_t *__restrict__ x,
+__global__ __launch_bounds__(64 * QLONG_WAVES) void qmv_long_kernel(int N, int K, const uint16_t *__restrict__ x,
                                                                     const uint8_t *__restrict__ w,
-                                                                    const uint8_t *__restrict__ s,
-                                                                    const YOut yo, int N, int K) {
+                                                                    const uint8_t *__restrict__ s, const YOut yo) {
   using L = XLayout<MODE>;
   constexpr int T = 64 * QLONG_WAVES;
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
@@ -770,8 +768,8 @@ static hipError_t launch_qmv_long_t(const QmmArgs &a, hipStream_t st) {
   const int per_cu = (int)(QMV_LONG_LDS_MAX / lds) < PER_CU ? (int)(QMV_LONG_LDS_MAX / lds) : PER_CU;
   const int want = ((a.N + R - 1) / R + QLONG_WAVES - 1) / QLONG_WAVES, have = cus * (per_cu > 0 ? per_cu : 1);
   dim3 grid(want < have ? want : have);
-  hipLaunchKernelGGL((qmv_long_kernel<MODE, M, ISEG, R>), grid, dim3(64 * QLONG_WAVES), lds, st, (const uint16_t *)a.x,
-                     a.w, a.s, yout_of(a), a.N, a.K);
+  hipLaunchKernelGGL((qmv_long_kernel<MODE, M, ISEG, R>), grid, dim3(64 * QLONG_WAVES), lds, st, a.N, a.K,
+                     (const uint16_t *)a.x, a.w, a.s, yout_of(a));
   return hipGetLastError();
 }
 
