@@ -26,11 +26,12 @@ FLAGS = [
 ]
 
 
-# Decode kernels: the leading kernel arguments (sizes and pointers, 16 dwords) arrive
-# preloaded in SGPRs, so a wave issues its first loads without a kernel-argument round
-# trip (gfx950 firmware; the code keeps a loading prologue for firmware without it).
+# Decode kernels (GEMVs, the GDN step): the leading kernel arguments (sizes and pointers,
+# up to 16 dwords) arrive preloaded in SGPRs, so a wave issues its first loads without a
+# kernel-argument round trip (gfx950 firmware; the code keeps a loading prologue for
+# firmware without it).
 PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
-EXTRA = {"qmv_mfma.hip": PRELOAD, "qmv.hip": PRELOAD}
+EXTRA = {"qmv_mfma.hip": PRELOAD, "qmv.hip": PRELOAD, "gdn.hip": PRELOAD}
 
 
 def _compile(src: str) -> Path:

@@ -191,11 +191,11 @@ __global__ __launch_bounds__(256) void gdn_kernel(const void *__restrict__ q, co
 constexpr int GDN_SHORT = 4;
 
 template <bool IN_F32, bool Y_F32>
-__global__ __launch_bounds__(256) void gdn_short_kernel(const void *__restrict__ q, const void *__restrict__ k,
-                                                        const void *__restrict__ v, const float *__restrict__ g,
-                                                        const void *__restrict__ beta, int beta_f32,
-                                                        const float *st_in, float *st_out, void *__restrict__ y,
-                                                        int T, int Hk, int Hv, int Dv) {
+__global__ __launch_bounds__(256) void gdn_short_kernel(int T, int Hk, int Hv, int Dv, int beta_f32,
+                                                        const float *st_in, const void *__restrict__ q,
+                                                        const void *__restrict__ k, const void *__restrict__ v,
+                                                        const float *__restrict__ g, const void *__restrict__ beta,
+                                                        float *st_out, void *__restrict__ y) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int groups = (Dv + 15) >> 4;
   const int nh = blockIdx.x / groups, grp = blockIdx.x - nh * groups;  // nh = b * Hv + hv
@@ -264,8 +264,8 @@ __global__ __launch_bounds__(256) void gdn_short_kernel(const void *__restrict__
 template <bool IN, bool YF>
 static void launch_gdn_t(const GdnArgs &a, unsigned grid, hipStream_t st) {
   if (a.T <= GDN_SHORT)
-    hipLaunchKernelGGL((gdn_short_kernel<IN, YF>), dim3(grid), dim3(256), 0, st, a.q, a.k, a.v, a.g, a.beta,
-                       (int)a.beta_f32, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv);
+    hipLaunchKernelGGL((gdn_short_kernel<IN, YF>), dim3(grid), dim3(256), 0, st, a.T, a.Hk, a.Hv, a.Dv,
+                       (int)a.beta_f32, a.state_in, a.q, a.k, a.v, a.g, a.beta, a.state_out, a.y);
   else if (a.T <= GDN_TB)
     hipLaunchKernelGGL((gdn_kernel<IN, YF, true>), dim3(grid), dim3(256), 0, st, a.q, a.k, a.v, a.g, a.beta,
                        (int)a.beta_f32, a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv);
