@@ -500,3 +500,39 @@ def test_prefill_scales_tiled_copy_kept_with_handle(mode):
     ref = O.qmm(mode, x.view(torch.int16).cpu().numpy().view(np.uint16), wq.numpy(), sc.numpy())
     ok, fro, worst = O.check_tolerance(f32(outs[-1].view(torch.int16).cpu().numpy().view(np.uint16)), f32(ref), **TOL)
     assert ok, (fro, worst)
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+def test_prefill_two_streams_at_once(mode):
+    """Prefill calls issued on two streams without synchronising between them: each stream
+    has its own workspace (the mxfp8 x split lives there), so the interleaved calls give the
+    same bits as the same calls run one after the other."""
+    import torch
+
+    M, N, K = 520, 2048, 2048
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(78)
+    W = (torch.randn((N, K), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    xs = [torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16) for _ in range(2)]
+    wq, sc = Q.quantize(Q.Array.from_torch(W), mode)
+    refs = [Q.quantized_matmul(Q.Array.from_torch(x), wq, sc, mode) for x in xs]
+    torch.cuda.synchronize()
+    refs = [torch.from_numpy(r.numpy().view(np.int16)) for r in refs]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[], []]
+    for _ in range(4):
+        for k in range(2):
+            with torch.cuda.stream(streams[k]):
+                y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+                Q.quantized_matmul(Q.Array.from_torch(xs[k]), wq, sc, mode, out=Q.Array.from_torch(y),
+                                   stream=Q.Stream.torch_current())
+                outs[k].append(y)
+    torch.cuda.synchronize()
+    for k in range(2):
+        for y in outs[k]:
+            assert torch.equal(y.view(torch.int16).cpu(), refs[k])
+    ref = O.qmm(mode, xs[1].view(torch.int16).cpu().numpy().view(np.uint16), wq.numpy(), sc.numpy(),
+                cols=np.arange(0, N, 7))
+    ok, fro, worst = O.check_tolerance(f32(refs[1].numpy().view(np.uint16)[:, ::7]), f32(ref), **TOL)
+    assert ok, (fro, worst)
