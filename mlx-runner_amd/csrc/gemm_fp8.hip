@@ -150,6 +150,17 @@ __global__ __launch_bounds__(256) void split_x_packed_kernel(const uint16_t *__r
   }
   const int rr = (int)(r & 255);
   const int64_t tile = (int64_t)(r >> 8) * (K >> 6);
+  const bool store = live && (int)r < rows;
+  // Scale bytes: step st0 + u of row r holds blocks 2 (st0 + u) + {0, 1} (lanes l % 4 in
+  // {0, 1}, {2, 3}); st0 is even, so steps u = 2P, 2P + 1 fill the four bytes of the row's
+  // tile-major dword st0 / 2 + P in block order.  Each lane packs the bytes of its own
+  // blocks and takes the other block's from lane l ^ 2; then lane l % 4 = 2 t + P stores
+  // whole dword P of hi (t = 0) or lo (t = 1) scales.
+  constexpr int PW = U / 2;
+  uint32_t ph[PW], pl[PW];
+#pragma unroll
+  for (int p = 0; p < PW; ++p) ph[p] = pl[p] = 0u;
+  const int hb = (int)((l >> 1) & 1);  // the lane's block within the step
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     uint32_t hw[4], lw[4];
@@ -157,16 +168,25 @@ __global__ __launch_bounds__(256) void split_x_packed_kernel(const uint16_t *__r
     split16(q[u][0], q[u][1], hw, lw, th, tl);
     const uint32_t c = 4 * (st0 + u) + (l & 3);
     const int b = (int)(c >> 1), j = (int)(c & 1);
-    if (live && (int)r < rows) {
+    const int sft = 8 * (2 * (u & 1) + hb);
+    ph[u >> 1] |= (uint32_t)(th + 127) << sft;
+    pl[u >> 1] |= (uint32_t)(tl + 127) << sft;
+    if (store) {
       const int64_t o = (tile + (b >> 1)) * 16384 + 16 * (4 * rr + ((2 * (b & 1) + j) ^ p_swz(rr)));
       *(uint4 *)(xh + o) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
       *(uint4 *)(xl + o) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-      if (j == 0) {
-        const int64_t so = packed_scale_index(r, b, K);
-        sh[so] = (uint8_t)(th + 127);
-        sl[so] = (uint8_t)(tl + 127);
-      }
     }
+  }
+#pragma unroll
+  for (int p = 0; p < PW; ++p) {
+    ph[p] |= (uint32_t)__shfl_xor((int)ph[p], 2);
+    pl[p] |= (uint32_t)__shfl_xor((int)pl[p], 2);
+  }
+  const int t = (int)((l >> 1) & 1), p = (int)(l & 1);
+  if (store && p < PW) {
+    const uint32_t v = PW == 1 ? (t ? pl[0] : ph[0]) : (t ? (p ? pl[PW - 1] : pl[0]) : (p ? ph[PW - 1] : ph[0]));
+    uint8_t *dst = t ? sl : sh;
+    *(uint32_t *)(dst + packed_scale_index(r, 2 * (st0 + 2 * p), K)) = v;
   }
 }
 
