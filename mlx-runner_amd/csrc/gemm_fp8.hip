@@ -591,20 +591,13 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
       e = launch_repack_scales(a.s, (int64_t)a.N, a.K / 32, (uint32_t *)swp, st);
       if (e != hipSuccess) return e;
     }
-    static bool pipe_attr_set = false;
-    static int cus = 0;
-    if (!pipe_attr_set) {
-      e = hipFuncSetAttribute((const void *)gemm_mxfp8_pipe_kernel<256>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)PipeGeom<256>::LDS);
-      if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void *)gemm_mxfp8_pipe_kernel<128>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)PipeGeom<128>::LDS);
-      int dev = 0;
-      if (e == hipSuccess) e = hipGetDevice(&dev);
-      if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-      if (e != hipSuccess) return e;
-      pipe_attr_set = true;
-    }
+    static std::atomic<uint64_t> lds256{0}, lds128{0};
+    e = ensure_dynamic_lds(lds256, (const void *)gemm_mxfp8_pipe_kernel<256>, (int)PipeGeom<256>::LDS);
+    if (e == hipSuccess)
+      e = ensure_dynamic_lds(lds128, (const void *)gemm_mxfp8_pipe_kernel<128>, (int)PipeGeom<128>::LDS);
+    if (e != hipSuccess) return e;
+    const int cus = device_cu_count();
+    if (cus <= 0) return hipErrorNoDevice;
     // One block per CU at a time (the ring fills most of a CU's LDS).  When the
     // 256-tiles leave a last round that a whole number of W tile-columns fills
     // and four times as many 128-tiles still fit one round, those columns run
@@ -626,13 +619,9 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
                        sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, n_split, a.N);
     return hipGetLastError();
   }
-  static bool attr_set = false;
-  if (!attr_set) {
-    e = hipFuncSetAttribute((const void *)gemm_mxfp8_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sizeof(Fp8Smem));
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  e = ensure_dynamic_lds(lds_set, (const void *)gemm_mxfp8_kernel, (int)sizeof(Fp8Smem));
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(gemm_mxfp8_kernel, dim3(tiles), dim3(F_THREADS), sizeof(Fp8Smem), st, xh, xl, sh, sl, a.w, a.s,
                      (uint16_t *)a.y, a.M, a.N, a.K);
   return hipGetLastError();

@@ -256,13 +256,9 @@ hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
     if (e != hipSuccess) return e;
     tiled = (const uint8_t *)ws;
   }
-  static bool attr_set = false;
-  if (!attr_set) {
-    e = hipFuncSetAttribute((const void *)gemm_nvfp4_pipe_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)V_LDS);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  e = ensure_dynamic_lds(lds_set, (const void *)gemm_nvfp4_pipe_kernel, (int)V_LDS);
+  if (e != hipSuccess) return e;
   const int tiles = ((a.M + V_BM - 1) / V_BM) * ((a.N + V_BN - 1) / V_BN);
   hipLaunchKernelGGL(gemm_nvfp4_pipe_kernel, dim3(tiles), dim3(V_THREADS), V_LDS, st, (const uint16_t *)a.x, a.w,
                      tiled, (uint16_t *)a.y, a.M, a.N, a.K);

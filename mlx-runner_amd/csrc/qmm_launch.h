@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace qmm {
 
 enum Mode : int { MXFP8 = 0, NVFP4 = 1 };
@@ -135,6 +137,15 @@ hipError_t launch_gdn_chunked_noalloc(const GdnArgs &a, hipStream_t st);
 
 // Zero-fill `bytes` of device memory.
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st);
+
+// Compute units of the current device, cached per device (0, with the HIP error
+// cleared, when no device answers: the caller's launch then reports the failure).
+int device_cu_count();
+// Raise a kernel's dynamic-LDS limit to `bytes` once per device.  `done` is the call
+// site's own mask of devices already set (one bit per device id below 64; higher ids
+// set it on every call).  Safe from several host threads: the attribute call is
+// idempotent and the mask is atomic.
+hipError_t ensure_dynamic_lds(std::atomic<uint64_t> &done, const void *kernel, int bytes);
 
 // Dense bf16 y[M, N] = x[M, K] @ w[N, K].T (fp32 accumulate, RNE).
 hipError_t launch_linear_bf16(const uint16_t *x, const uint16_t *w, uint16_t *y, int M, int N, int K,

@@ -479,19 +479,8 @@ static hipError_t launch_qmv_bf16_t(const QmmArgs &a, hipStream_t st) {
 // (24 rows) and half two, in 1024 5-wave ones every CU gets four (20 rows).
 // Measured at mxfp8 N = K = 5120 (one box, per-wave timestamps): 6.91 -> 6.57 us;
 // 10-wave workgroups (two per CU) gained nothing and 4-wave ones slightly less.
-static int qmv_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-      cus = n;
-    else
-      (void)hipGetLastError();  // no device: the caller's launch reports it
-  }
-  return cus;
-}
 static bool qmv_five_waves(int N) {
-  const int cus = qmv_cus();
+  const int cus = device_cu_count();
   if (cus <= 0) return false;
   auto max_rows = [&](int wv) {  // rows of the most loaded CU
     const int64_t grid = (N + (int64_t)wv - 1) / wv;
@@ -753,18 +742,12 @@ constexpr size_t QMV_LONG_LDS_MAX = 156 * 1024;
 template <int MODE, int M, int ISEG, int R, int PER_CU>
 static hipError_t launch_qmv_long_t(const QmmArgs &a, hipStream_t st) {
   const size_t lds = qmv_long_lds(MODE, M, a.K);
-  static bool attr_set = false;
-  static int cus = 0;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)qmv_long_kernel<MODE, M, ISEG, R>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)QMV_LONG_LDS_MAX);
-    if (e != hipSuccess) return e;
-    int dev = 0;
-    e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  const hipError_t e =
+      ensure_dynamic_lds(lds_set, (const void *)qmv_long_kernel<MODE, M, ISEG, R>, (int)QMV_LONG_LDS_MAX);
+  if (e != hipSuccess) return e;
+  const int cus = device_cu_count();
+  if (cus <= 0) return hipErrorNoDevice;
   const int per_cu = (int)(QMV_LONG_LDS_MAX / lds) < PER_CU ? (int)(QMV_LONG_LDS_MAX / lds) : PER_CU;
   const int want = ((a.N + R - 1) / R + QLONG_WAVES - 1) / QLONG_WAVES, have = cus * (per_cu > 0 ? per_cu : 1);
   dim3 grid(want < have ? want : have);

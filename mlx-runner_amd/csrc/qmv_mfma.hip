@@ -646,17 +646,7 @@ static QfShape qf_shape(int K) {
   }
 }
 
-static int qf_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-      cus = n;
-    else
-      (void)hipGetLastError();  // no device: the caller's launch reports it
-  }
-  return cus;
-}
+static int qf_cus() { return device_cu_count(); }
 
 // Units per workgroup: row blocks of 16 rows (8 output rows in the MLP form).
 static int qf_nrb(const QmmArgs &a, int cus, int nmat = 1) {
@@ -720,12 +710,9 @@ static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *
                             hipStream_t st) {
   auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D, P, PARTS>;
   const size_t lds = qf_lds_bytes<MODE>(M, Q, F);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  const hipError_t e = ensure_dynamic_lds(lds_set, (const void *)kern, 160 * 1024);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), lds, st, a.N, a.K, F, a.N / grid, a.N % grid,
                      (const uint16_t *)a.x, a.w, a.s, w2, s2, yout_of(a));
   return hipGetLastError();
@@ -777,12 +764,9 @@ template <int M, int Q, int P, int NMAT, bool PARTS = false>
 static hipError_t launch_q32(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
                              hipStream_t st) {
   auto kern = qmv_mfma32_kernel<M, Q, P, NMAT, PARTS>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  const hipError_t e = ensure_dynamic_lds(lds_set, (const void *)kern, 160 * 1024);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), q32_lds_bytes(M, Q, F), st, a.N, a.K, F, a.N / grid,
                      a.N % grid, (const uint16_t *)a.x, a.w, a.s, w2, s2, yout_of(a));
   return hipGetLastError();

@@ -536,3 +536,54 @@ def test_prefill_two_streams_at_once(mode):
                 cols=np.arange(0, N, 7))
     ok, fro, worst = O.check_tolerance(f32(refs[1].numpy().view(np.uint16)[:, ::7]), f32(ref), **TOL)
     assert ok, (fro, worst)
+
+
+def test_calls_from_several_host_threads():
+    """Four host threads, each with its own stream, issue decode and prefill calls of both
+    modes at the same time (the binding releases the GIL inside the library): every output
+    equals the same call run alone, bit for bit."""
+    import threading
+
+    import torch
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(91)
+    K, N = 1024, 1536
+    W = (torch.randn((N, K), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    quant = {mode: Q.quantize(Q.Array.from_torch(W), mode) for mode in ("mxfp8", "nvfp4")}
+    cases = [(mode, M) for mode in ("mxfp8", "nvfp4") for M in (1, 3, 300)]
+    xs = {M: torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16) for M in (1, 3, 300)}
+    refs = {}
+    for mode, M in cases:
+        wq, sc = quant[mode]
+        refs[mode, M] = Q.quantized_matmul(Q.Array.from_torch(xs[M]), wq, sc, mode).numpy().view(np.int16)
+    torch.cuda.synchronize()
+    outs, errors = {}, []
+
+    def worker(t):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for rep in range(3):
+                    for mode, M in cases[t % 2:] + cases[:t % 2]:
+                        wq, sc = quant[mode]
+                        y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+                        Q.quantized_matmul(Q.Array.from_torch(xs[M]), wq, sc, mode, out=Q.Array.from_torch(y),
+                                           stream=Q.Stream.torch_current())
+                        outs[t, rep, mode, M] = y
+            s.synchronize()
+        except Exception as e:  # reported by the main thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    assert len(outs) == 4 * 3 * len(cases)
+    for (t, rep, mode, M), y in outs.items():
+        assert np.array_equal(y.view(torch.int16).cpu().numpy(), refs[mode, M]), (t, rep, mode, M)
+    assert Q.take_error() is None
