@@ -4,6 +4,8 @@ Bars: dequant and quantize bit-exact; qmm bf16 outputs within relative
 Frobenius 1e-3 and max-abs 4 bf16 ulp of each row's max |y| (oracle rounds its
 double sum once to bf16); f32 outputs within the same bound.
 """
+import functools
+
 import numpy as np
 import pytest
 
@@ -587,3 +589,41 @@ def test_calls_from_several_host_threads():
     for (t, rep, mode, M), y in outs.items():
         assert np.array_equal(y.view(torch.int16).cpu().numpy(), refs[mode, M]), (t, rep, mode, M)
     assert Q.take_error() is None
+
+
+@functools.lru_cache(maxsize=2)
+def _nf_weights(mode, N, K):
+    return rand_w(np.random.default_rng(4242), mode, N, K)
+
+
+# Non-finite x: the reference multiplies dequantized weights by x in floating point, so a
+# NaN in row m of x makes every output of row m NaN, and an infinity makes every output
+# of the row non-finite (±inf, or NaN where the weight is zero); the other rows are
+# unaffected.  Every kernel family: the unpacking GEMV, the MFMA GEMV (16x16x128 and
+# 32x32x64 forms, one and several passes), the long-row GEMV and both prefill GEMMs.
+@pytest.mark.parametrize("bad", ["nan", "inf", "-inf"])
+@pytest.mark.parametrize("mode,M,N,K", [
+    ("mxfp8", 1, 5120, 5120), ("nvfp4", 1, 5120, 5120), ("nvfp4", 1, 16400, 5120), ("nvfp4", 2, 4099, 5120),
+    ("nvfp4", 3, 4099, 5120), ("mxfp8", 3, 4096, 5120), ("nvfp4", 1, 5120, 17408), ("nvfp4", 3, 5120, 17408),
+    ("mxfp8", 1, 2048, 17408), ("mxfp8", 2, 5120, 17408), ("mxfp8", 300, 1000, 1024), ("nvfp4", 300, 1000, 1024)])
+def test_non_finite_x_propagates_to_its_row(mode, M, N, K, bad):
+    wq, s = _nf_weights(mode, N, K)
+    xb = make_x(np.random.default_rng(4243), M, K, "normal")
+    code = {"nan": 0x7FC0, "inf": 0x7F80, "-inf": 0xFF80}[bad]
+    xb[0, 37] = code                      # one element of row 0
+    if M > 1:
+        xb[M - 1, K - 5] = code           # and one near the end of the last row
+    y = run_qmm(mode, xb, wq, s)
+    yf = f32(y)
+    bad_rows = [0] + ([M - 1] if M > 1 else [])
+    for m in bad_rows:
+        if bad == "nan":
+            assert np.isnan(yf[m]).all(), (m, int(np.isfinite(yf[m]).sum()))
+        else:
+            assert not np.isfinite(yf[m]).any(), (m, int(np.isfinite(yf[m]).sum()))
+    good = [m for m in range(M) if m not in bad_rows]
+    if good:
+        cols = np.arange(0, N, 7)
+        ref = O.qmm(mode, xb[good], wq, s, cols=cols)
+        ok, fro, worst = O.check_tolerance(f32(y[good][:, cols]), f32(ref), **TOL)
+        assert ok, (fro, worst)
