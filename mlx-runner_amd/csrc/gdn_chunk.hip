@@ -116,19 +116,6 @@ __device__ __forceinline__ float ld1f(const void *p, int64_t i) {
     return bf16_to_f32(((const uint16_t *)p)[i]);
 }
 
-// 32 bf16 (four 16-byte pieces) as f32
-__device__ __forceinline__ void unpack32(const uint4 (&p)[4], float *o) {
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const uint32_t wv[4] = {p[u].x, p[u].y, p[u].z, p[u].w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o[8 * u + 2 * j] = __uint_as_float(wv[j] << 16);
-      o[8 * u + 2 * j + 1] = __uint_as_float(wv[j] & 0xFFFF0000u);
-    }
-  }
-}
-
 // e^x from an f64 argument: 2^(x log2 e) split into an integer and a fraction in [0, 1);
 // the fraction's power on v_exp_f32, the integer on the exponent (underflow gives 0)
 __device__ __forceinline__ float exp_f64arg(double x) {
@@ -310,7 +297,7 @@ constexpr size_t SCAN_LDS = (size_t)(GR * KP + KT_SIZE + 2 * GR * TP) * 4;
 // and columns 32 w .. 32 w + 31 of the state.  Lane l's A operands (row 16 w + l % 16 of
 // K, Q, Ap and M over its lane group's run of columns) come straight from global memory
 // into registers, one chunk ahead.
-template <bool IN_F32, bool Y_F32>
+template <bool Y_F32>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_chunk_scan(
     const void *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v, const float *__restrict__ ws,
     const float *st_in, float *st_out, void *__restrict__ y, int T, int Hk, int Hv, int Dv, int nch, int nwg) {
@@ -334,10 +321,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   for (int e = tid; e < GR * GDK; e += 256) s_s[(e / GDK) * KP + e % GDK] = sin[e];
 
-  // one chunk ahead, in registers: the Ap and M runs, Q and K row runs (bf16 inputs; f32 ones are read in the chunk, to stay
-  // within 256 registers), V at this lane's output positions, gam, tail
+  // one chunk ahead, in registers: the Ap and M runs, V at this lane's output positions,
+  // gam, tail (the f32 Q and K rows are read in the chunk, to stay within 256 registers)
   float4 pap[4], pm[4];
-  uint4 pq[4], pk[4];
   float pv[4], pg, ptl, pgl;
   auto qk_off = [&](int ci) __attribute__((always_inline)) {
     const int t0 = ci * GC, n = T - t0 < GC ? T - t0 : GC;
@@ -367,36 +353,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     pg = cw[WS_GAM + tr];
     ptl = cw[WS_TAIL + tr];
     pgl = cw[WS_GAM + GC - 1];
-    if constexpr (!IN_F32) {
-      const int64_t qo = qk_off(ci);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) pq[u] = ((const uint4 *)((const uint16_t *)q + qo))[u];
-    }
 #pragma unroll
     for (int vv = 0; vv < 4; ++vv) {
       const int t = 16 * wave + 4 * lg + vv, tt = t < n ? t : n - 1;
-      pv[vv] = ld1f<IN_F32>(v, (((int64_t)b * T + t0 + tt) * Hv + hv) * Dv + r0 + li);
+      pv[vv] = ld1f<true>(v, (((int64_t)b * T + t0 + tt) * Hv + hv) * Dv + r0 + li);
     }
   };
-  auto load_k = [&](int ci) __attribute__((always_inline)) {
-    if constexpr (!IN_F32) {
-      const int64_t ko = qk_off(ci);
+  auto k_row = [&](int ci, float *o) __attribute__((always_inline)) {  // this lane's K run
+    const int64_t ko = qk_off(ci);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) pk[u] = ((const uint4 *)((const uint16_t *)k + ko))[u];
-    }
-  };
-  auto k_row = [&](int ci, float *o) __attribute__((always_inline)) {  // this lane's K run as f32
-    if constexpr (IN_F32) {
-      const int64_t ko = qk_off(ci);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) ld8f<true>(k, ko + 8 * u, o + 8 * u);
-    } else {
-      unpack32(pk, o);
-    }
+    for (int u = 0; u < 4; ++u) ld8f<true>(k, ko + 8 * u, o + 8 * u);
   };
 
   load_q(0);
-  load_k(0);
   load_ap(0);
   load_m(0);
   // one chunk; FULL chunks (all 64 steps within T) store every y row unconditionally
@@ -412,12 +381,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     k_row(ci, ak);
 #pragma unroll
     for (int m = 0; m < 32; ++m) ak[m] *= -gq;
-    if constexpr (IN_F32) {
+    {
       const int64_t qo = qk_off(ci);
 #pragma unroll
       for (int u = 0; u < 4; ++u) ld8f<true>(q, qo + 8 * u, aq + 8 * u);
-    } else {
-      unpack32(pq, aq);
     }
 #pragma unroll
     for (int m = 0; m < 32; ++m) aq[m] *= gq;
@@ -441,7 +408,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int j = 0; j < 32; ++j) kt_s[kt_at(32 * lg + j, tr)] = tl * kr[j];
     }
-    load_k(cn);
     __builtin_amdgcn_sched_barrier(0);
     // Dl = Ap U
     float ub[16];
@@ -746,7 +712,7 @@ static hipError_t launch_chunked_t(const GdnArgs &a, float *ws, hipStream_t st) 
   const int nwg = (int)(nh * (a.Dv / GR));
   const dim3 grid((unsigned)((nwg + 7) / 8 * 8));
   if constexpr (IN)
-    hipLaunchKernelGGL((gdn_chunk_scan<true, YF>), grid, dim3(256), SCAN_LDS, st, a.q, a.k, a.v, (const float *)ws,
+    hipLaunchKernelGGL((gdn_chunk_scan<YF>), grid, dim3(256), SCAN_LDS, st, a.q, a.k, a.v, (const float *)ws,
                        a.state_in, a.state_out, a.y, a.T, a.Hk, a.Hv, a.Dv, nch, nwg);
   else
     hipLaunchKernelGGL((gdn_chunk_scan_bf<YF>), grid, dim3(256), SCANB_LDS, st, a.q, a.k, a.v, (const float *)ws,
