@@ -627,3 +627,35 @@ def test_non_finite_x_propagates_to_its_row(mode, M, N, K, bad):
         ref = O.qmm(mode, xb[good], wq, s, cols=cols)
         ok, fro, worst = O.check_tolerance(f32(y[good][:, cols]), f32(ref), **TOL)
         assert ok, (fro, worst)
+
+
+def test_random_shapes_match_oracle():
+    """40 seeded random (mode, M, N, K, x dtype) draws across every dispatch boundary (M in
+    1..700, N in 1..6000, K any multiple of the mode's group up to 6144, x bf16 or f32),
+    each against the oracle on a column sample.  A draw that fails names itself."""
+    import torch
+
+    rng = np.random.default_rng(20261202)
+    draws = []
+    for _ in range(40):
+        mode = str(rng.choice(["mxfp8", "nvfp4"]))
+        grp = 32 if mode == "mxfp8" else 16
+        M = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 9, 17, 64, 255, 256, 257, 700]))
+        N = int(rng.integers(1, 6000))
+        K = grp * int(rng.integers(1, 6144 // grp + 1))
+        x_f32 = bool(rng.random() < 0.2)
+        draws.append((mode, M, N, K, x_f32))
+    for mode, M, N, K, x_f32 in draws:
+        case = f"{mode} M={M} N={N} K={K} x_f32={x_f32}"
+        print(f"[random] {case}", flush=True)
+        wq, s = rand_w(rng, mode, N, K)
+        xb = make_x(rng, M, K, "normal")
+        xin = f32(xb) if x_f32 else xb
+        y = run_qmm(mode, xin, wq, s, x_f32=x_f32)
+        cols = np.unique(np.concatenate([np.arange(0, N, max(1, N // 97)), [N - 1]]))
+        ref = O.qmm(mode, xb, wq, s, cols=cols, out="f32" if x_f32 else "bf16")
+        got = y[:, cols] if x_f32 else f32(y[:, cols])
+        want = ref if x_f32 else f32(ref)
+        ok, fro, worst = O.check_tolerance(got.astype(np.float32), want.astype(np.float32), **TOL)
+        assert ok, (case, fro, worst)
+    torch.cuda.synchronize()
