@@ -362,12 +362,12 @@ __device__ __forceinline__ i32x8_t p_frag(const uint8_t *base, int off) {
   return i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
 }
 
-// Covers x rows [0, M) and W rows [n_begin, n_end) in TS x TS tiles.
+// Tile `bid` of the TS x TS tiling of x rows [0, M) and W rows [n_begin, n_end).
 template <int TS>
-__global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
-    const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
-    const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
-    uint16_t *__restrict__ y, int M, int N, int K, int n_begin, int n_end) {
+__device__ __forceinline__ void pipe_tile(int bid, const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl,
+                                          const uint8_t *__restrict__ sh, const uint8_t *__restrict__ sl,
+                                          const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
+                                          uint16_t *__restrict__ y, int M, int N, int K, int n_begin, int n_end) {
   using G = PipeGeom<TS>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t lds0 = lds_addr(lds);
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;  // wave tile: rows wm * TS / 4 + [0, TS / 4), cols wn * TS / 2 + [0, TS / 2)
   int tm, tn;
-  tile_of(blockIdx.x, (M + TS - 1) / TS, (n_end - n_begin + TS - 1) / TS, &tm, &tn);
+  tile_of(bid, (M + TS - 1) / TS, (n_end - n_begin + TS - 1) / TS, &tm, &tn);
   const int m0 = tm * TS, n0 = n_begin + tn * TS;
   const int steps = K / P_BK;
 
@@ -517,6 +517,31 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
                                              n0 + wn * (TS / 2), n_end, vec);
 }
 
+// Covers x rows [0, M) and W rows [n_begin, n_end) in TS x TS tiles.
+template <int TS>
+__global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
+    const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
+    const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
+    uint16_t *__restrict__ y, int M, int N, int K, int n_begin, int n_end) {
+  pipe_tile<TS>(blockIdx.x, xh, xl, sh, sl, w, sw, y, M, N, K, n_begin, n_end);
+}
+
+// Both tilings in one launch: blocks [0, tiles1) are the 256-tiles of W rows [0, n_split),
+// the rest the 128-tiles of W rows [n_split, N).  Blocks start in index order as CUs
+// free up, so a CU that finishes its last 256-tile early takes a 128-tile at once
+// instead of waiting for the slowest CU at a kernel boundary.  (tiles1 is a multiple
+// of 8, so both parts keep their XCD-aware tile order.)
+__global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_split_kernel(
+    const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
+    const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
+    uint16_t *__restrict__ y, int M, int N, int K, int n_split, int tiles1) {
+  const int b = blockIdx.x;
+  if (b < tiles1)
+    pipe_tile<256>(b, xh, xl, sh, sl, w, sw, y, M, N, K, 0, n_split);
+  else
+    pipe_tile<128>(b - tiles1, xh, xl, sh, sl, w, sw, y, M, N, K, n_split, N);
+}
+
 // K % 128: whole step pairs (the tile-major scale layout); W rows must be 16-byte
 // aligned for the DMA, and the W scales 4-byte aligned for the repack.
 static bool gemm_mxfp8_pipe_ok(const QmmArgs &a) {
@@ -591,10 +616,12 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
       e = launch_repack_scales(a.s, (int64_t)a.N, a.K / 32, (uint32_t *)swp, st);
       if (e != hipSuccess) return e;
     }
-    static std::atomic<uint64_t> lds256{0}, lds128{0};
+    static std::atomic<uint64_t> lds256{0}, lds128{0}, lds_split{0};
     e = ensure_dynamic_lds(lds256, (const void *)gemm_mxfp8_pipe_kernel<256>, (int)PipeGeom<256>::LDS);
     if (e == hipSuccess)
       e = ensure_dynamic_lds(lds128, (const void *)gemm_mxfp8_pipe_kernel<128>, (int)PipeGeom<128>::LDS);
+    if (e == hipSuccess)
+      e = ensure_dynamic_lds(lds_split, (const void *)gemm_mxfp8_pipe_split_kernel, (int)PipeGeom<256>::LDS);
     if (e != hipSuccess) return e;
     const int cus = device_cu_count();
     if (cus <= 0) return hipErrorNoDevice;
@@ -610,11 +637,21 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
       n_split = (tiles_n - cols) * 256;
     }
     const int tiles1 = tiles_m * ((n_split + 255) / 256);
+    if (n_split == a.N) {
+      hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel<256>, dim3(tiles1), dim3(F_THREADS), PipeGeom<256>::LDS, st, xh, xl,
+                         sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, 0, n_split);
+      return hipGetLastError();
+    }
+    const int tiles2 = ((a.M + 127) / 128) * ((a.N - n_split + 127) / 128);
+    if (tiles1 % 8 == 0) {
+      hipLaunchKernelGGL(gemm_mxfp8_pipe_split_kernel, dim3(tiles1 + tiles2), dim3(F_THREADS), PipeGeom<256>::LDS, st,
+                         xh, xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, n_split, tiles1);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel<256>, dim3(tiles1), dim3(F_THREADS), PipeGeom<256>::LDS, st, xh, xl, sh,
                        sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, 0, n_split);
     e = hipGetLastError();
-    if (e != hipSuccess || n_split == a.N) return e;
-    const int tiles2 = ((a.M + 127) / 128) * ((a.N - n_split + 127) / 128);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel<128>, dim3(tiles2), dim3(F_THREADS), PipeGeom<128>::LDS, st, xh, xl, sh,
                        sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, n_split, a.N);
     return hipGetLastError();
