@@ -529,8 +529,9 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
 // Both tilings in one launch: blocks [0, tiles1) are the 256-tiles of W rows [0, n_split),
 // the rest the 128-tiles of W rows [n_split, N).  Blocks start in index order as CUs
 // free up, so a CU that finishes its last 256-tile early takes a 128-tile at once
-// instead of waiting for the slowest CU at a kernel boundary.  (tiles1 is a multiple
-// of 8, so both parts keep their XCD-aware tile order.)
+// instead of waiting for the slowest CU at a kernel boundary.  (The host gives tiles1
+// as whole rounds, a multiple of the CU count, so on a CU count that is a multiple of 8
+// both parts keep their XCD-aware tile order; any tiles1 gives the same results.)
 __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_split_kernel(
     const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
     const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
@@ -616,10 +617,8 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
       e = launch_repack_scales(a.s, (int64_t)a.N, a.K / 32, (uint32_t *)swp, st);
       if (e != hipSuccess) return e;
     }
-    static std::atomic<uint64_t> lds256{0}, lds128{0}, lds_split{0};
+    static std::atomic<uint64_t> lds256{0}, lds_split{0};
     e = ensure_dynamic_lds(lds256, (const void *)gemm_mxfp8_pipe_kernel<256>, (int)PipeGeom<256>::LDS);
-    if (e == hipSuccess)
-      e = ensure_dynamic_lds(lds128, (const void *)gemm_mxfp8_pipe_kernel<128>, (int)PipeGeom<128>::LDS);
     if (e == hipSuccess)
       e = ensure_dynamic_lds(lds_split, (const void *)gemm_mxfp8_pipe_split_kernel, (int)PipeGeom<256>::LDS);
     if (e != hipSuccess) return e;
@@ -643,17 +642,8 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
       return hipGetLastError();
     }
     const int tiles2 = ((a.M + 127) / 128) * ((a.N - n_split + 127) / 128);
-    if (tiles1 % 8 == 0) {
-      hipLaunchKernelGGL(gemm_mxfp8_pipe_split_kernel, dim3(tiles1 + tiles2), dim3(F_THREADS), PipeGeom<256>::LDS, st,
-                         xh, xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, n_split, tiles1);
-      return hipGetLastError();
-    }
-    hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel<256>, dim3(tiles1), dim3(F_THREADS), PipeGeom<256>::LDS, st, xh, xl, sh,
-                       sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, 0, n_split);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel<128>, dim3(tiles2), dim3(F_THREADS), PipeGeom<128>::LDS, st, xh, xl, sh,
-                       sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, n_split, a.N);
+    hipLaunchKernelGGL(gemm_mxfp8_pipe_split_kernel, dim3(tiles1 + tiles2), dim3(F_THREADS), PipeGeom<256>::LDS, st, xh,
+                       xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, n_split, tiles1);
     return hipGetLastError();
   }
   static std::atomic<uint64_t> lds_set{0};
