@@ -659,3 +659,24 @@ def test_random_shapes_match_oracle():
         ok, fro, worst = O.check_tolerance(got.astype(np.float32), want.astype(np.float32), **TOL)
         assert ok, (case, fro, worst)
     torch.cuda.synchronize()
+
+
+# mxfp8 prefill shapes whose 256 x 256 tiles leave a partial last round that whole W
+# tile-columns fill: those columns run as 128 x 128 tiles in the same launch.  M = 2000
+# (8 row tiles, the last one ragged) with N = 8448 (33 tile-columns: 264 tiles, 8 left
+# over = one column) and N = 8704 (34 columns: 272 tiles, 16 left over = two columns).
+@pytest.mark.parametrize("M,N", [(2000, 8448), (2048, 8704)])
+def test_prefill_with_tail_tiles_in_one_launch(M, N):
+    mode, K = "mxfp8", 640
+    rng = np.random.default_rng(M + N)
+    wq, s = rand_w(rng, mode, N, K)
+    xb = make_x(rng, M, K, "edge")
+    y = run_qmm(mode, xb, wq, s)
+    # every column of the last 640 (the tail tile-columns on a 256-CU part and their
+    # neighbours), plus a sample of the rest
+    cols = np.unique(np.concatenate([np.arange(N - 640, N), np.arange(0, N - 640, 37)]))
+    rows = np.unique(np.concatenate([np.arange(0, M, 61), [M - 1]]))
+    ref = O.qmm(mode, xb[rows], wq, s, cols=cols)
+    ok, fro, worst = O.check_tolerance(f32(y[rows][:, cols]), f32(ref), **TOL)
+    assert ok, (fro, worst)
+    assert np.isfinite(f32(y)).all()
