@@ -680,3 +680,24 @@ def test_prefill_with_tail_tiles_in_one_launch(M, N):
     ok, fro, worst = O.check_tolerance(f32(y[rows][:, cols]), f32(ref), **TOL)
     assert ok, (fro, worst)
     assert np.isfinite(f32(y)).all()
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+def test_empty_and_one_dimensional_x(mode):
+    """x with no rows ([0, K], [2, 0, K]) gives an empty result of the inferred shape and
+    no error; a 1-D x [K] gives [N], the same values as x[None, :] (MLX's shape rules)."""
+    rng = np.random.default_rng(77)
+    N, K = 96, 512
+    wq, s = rand_w(rng, mode, N, K)
+    w = Q.Array.from_numpy(wq, Q.UINT32)
+    sc = Q.Array.from_numpy(s, Q.UINT8)
+    for shape in [(0, K), (2, 0, K)]:
+        y = Q.quantized_matmul(Q.Array.from_numpy(np.zeros(shape, np.uint16), Q.BFLOAT16), w, sc, mode)
+        assert tuple(y.shape) == shape[:-1] + (N,)
+        assert y.numpy().size == 0
+    x1 = make_x(rng, 1, K, "normal")[0]
+    y1 = Q.quantized_matmul(Q.Array.from_numpy(x1, Q.BFLOAT16), w, sc, mode)
+    assert tuple(y1.shape) == (N,)
+    y2 = run_qmm(mode, x1[None, :], wq, s)
+    assert np.array_equal(y1.numpy(), y2[0])
+    assert Q.take_error() is None
