@@ -563,6 +563,8 @@ hipError_t launch_repack_scales(const uint8_t *s, int64_t N, int nb, uint32_t *o
   return hipGetLastError();
 }
 
+int gemm_mxfp8_split_layout_of(const QmmArgs &a) { return gemm_mxfp8_pipe_ok(a) ? 1 : 0; }
+
 bool gemm_mxfp8_ok(const QmmArgs &a) {
   return a.mode == MXFP8 && !a.x_f32 && a.K % F_BK == 0 && a.K > 0 && a.M > 0 && a.N > 0;
 }
@@ -598,7 +600,9 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
   const int64_t total = rows_t * (a.K / 16) / (pipe ? U : 1);
   if (rows_t * (a.K / 16) >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   const unsigned sb = (unsigned)((total + 255) / 256);
-  if (pipe && U == 4)
+  if (a.x_split_ready)
+    ;  // the previous call on this stream left this x split in this workspace
+  else if (pipe && U == 4)
     hipLaunchKernelGGL(split_x_packed_kernel<4>, dim3(sb), dim3(256), 0, st, (const uint16_t *)a.x, (uint32_t)total,
                        a.M, a.K, xh, xl, sh, sl);
   else if (pipe)

@@ -932,6 +932,11 @@ int qmm_mlp_gate_up_silu(qmm_array *res, qmm_array x, qmm_array w_gate, qmm_arra
   void *g = ws, *u = (char *)ws + bytes, *gws = gemm_ws ? (char *)ws + 2 * bytes : nullptr;
   a.y = g;
   b.y = u;
+  // mxfp8: the up projection reuses the x split the gate projection made in the shared
+  // workspace (same x, M, K and split layout; the two launches are stream-ordered)
+  const bool aligned_x = (((uintptr_t)a.x | (uintptr_t)a.w | (uintptr_t)b.w) & 15) == 0;
+  b.x_split_ready = gws && aligned_x && gemm_mxfp8_ok(a) && gemm_mxfp8_ok(b) &&
+                    gemm_mxfp8_split_layout_of(a) == gemm_mxfp8_split_layout_of(b);
   int rc = run_qmm(a, bytes, st, op, gws);
   if (!rc) rc = run_qmm(b, bytes, st, op, gws);
   if (!rc) {

@@ -46,6 +46,10 @@ struct QmmArgs {
   // The scales already in the prefill GEMMs' tile-major layout (the repack of
   // launch_repack_scales), or null: the GEMM then repacks them into its workspace.
   const uint32_t *s_tiled = nullptr;
+  // mxfp8 prefill: x is already split into this call's workspace (the previous call on the
+  // stream split the same x with the same M and K into the same workspace, for the same
+  // kernel family: gemm_mxfp8_split_layout_of of both calls agree), so the split is skipped.
+  bool x_split_ready = false;
 };
 
 // The output descriptor of a call: y as one part, or the grouped call's parts.
@@ -90,6 +94,9 @@ hipError_t launch_gemm(const QmmArgs &a, hipStream_t st);
 // mxfp8 prefill on the scaled fp8 MFMA (bf16 x split into E4M3 hi + lo).
 bool gemm_mxfp8_ok(const QmmArgs &a);
 size_t gemm_mxfp8_workspace(const QmmArgs &a);
+// The layout launch_gemm_mxfp8 splits x into (0: row-major, 1: pre-tiled for the pipelined
+// kernel); two calls may share one split only where this agrees.
+int gemm_mxfp8_split_layout_of(const QmmArgs &a);
 hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *workspace, hipStream_t st);
 bool gemm_nvfp4_ok(const QmmArgs &a);
 size_t gemm_nvfp4_workspace(const QmmArgs &a);
