@@ -35,14 +35,23 @@ namespace qmm {
 
 namespace {
 constexpr int V_BM = 256, V_BN = 256, V_BK = 64, V_THREADS = 512;
-constexpr int V_ATILE = 256 * 128;                 // x: 256 rows x 64 bf16
-constexpr int V_WTILE = 256 * 32;                  // W: 256 rows x 64 nvfp4
-constexpr int V_STILE = 1024;                      // scale dwords
-constexpr int V_STAGE = V_ATILE + V_WTILE + V_STILE;  // 41 KiB
+constexpr int V_WTILE = 256 * 32;  // W: 256 rows x 64 nvfp4
+constexpr int V_STILE = 1024;      // scale dwords
 constexpr int V_STAGES = 3;
-constexpr size_t V_LDS = (size_t)V_STAGES * V_STAGE;  // 123 KiB
-// DMAs per wave per step: 4 x, 1 W, and for wave 0 the step's 256 scale dwords (1 KiB, one DMA)
-constexpr int V_DMA_S = 6, V_DMA = 5;
+// Per x-tile height TM (256, or 128 for the last tile-columns of a call): the x tile,
+// TM rows x 64 bf16, one stage, the ring, the x fragments per wave (FI, of 32 rows), and
+// the DMAs per wave per step: FI x, 1 W, and for wave 0 the step's 256 scale dwords
+// (1 KiB, one DMA).
+template <int TM>
+struct NvGeom {
+  static constexpr int ATILE = TM * 128;
+  static constexpr int STAGE = ATILE + V_WTILE + V_STILE;  // 41 KiB at 256, 25 KiB at 128
+  static constexpr size_t LDS = (size_t)V_STAGES * STAGE;  // 123 KiB at 256
+  static constexpr int FI = TM / 64;
+  static constexpr int DMA = FI + 1, DMA_S = FI + 2;
+};
+// Every launch allocates the 256-row ring (the two-height kernel runs both in one launch).
+constexpr size_t V_LDS = NvGeom<256>::LDS;
 }  // namespace
 
 __device__ __forceinline__ int aswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
@@ -70,25 +79,29 @@ __device__ __forceinline__ bf16x8_t deq8_nvfp4(uint32_t word, uint32_t scale_byt
   return r;
 }
 
-__global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16_t *__restrict__ x,
-                                                                    const uint8_t *__restrict__ w,
-                                                                    const uint8_t *__restrict__ sp,
-                                                                    uint16_t *__restrict__ y, int M, int N, int K) {
+// Tile `bid` of the TM x 256 tiling of x rows [0, M) and W rows [n_begin, n_end)
+// (n_begin a multiple of 256).
+template <int TM>
+__device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x, const uint8_t *__restrict__ w,
+                                        const uint8_t *__restrict__ sp, uint16_t *__restrict__ y, int M, int N, int K,
+                                        int n_begin, int n_end) {
+  using G = NvGeom<TM>;
+  constexpr int FI = G::FI, WM = TM / 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t lds0 = lds_addr(lds);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;  // wave tile: rows wm * 128 + [0, 128), cols wn * 64 + [0, 64)
+  const int wm = wave & 1, wn = wave >> 1;  // wave tile: rows wm * WM + [0, WM), cols wn * 64 + [0, 64)
   int tm, tn;
-  tile_of(blockIdx.x, (M + V_BM - 1) / V_BM, (N + V_BN - 1) / V_BN, &tm, &tn);
-  const int m0 = tm * V_BM, n0 = tn * V_BN;
+  tile_of(bid, (M + TM - 1) / TM, (n_end - n_begin + V_BN - 1) / V_BN, &tm, &tn);
+  const int m0 = tm * TM, n0 = n_begin + tn * V_BN;
   const int steps = K / V_BK;
   const int64_t wrow = K >> 1;  // bytes per W row
 
   // DMA sources (step 0).  x: wave-instruction g = wave + 8 i fills slots q = 64 g + lane.
-  const uint8_t *ga[4];
+  const uint8_t *ga[FI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < FI; ++i) {
     const int g = wave + 8 * i;
     const int q = 64 * g + lane, row = q >> 3, part = (q & 7) ^ aswz(row);
     ga[i] = (const uint8_t *)x + ((int64_t)min(m0 + row, M - 1) * K + part * 8) * 2;
@@ -98,37 +111,37 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
   const int wr = 32 * wave + (lane >> 1);
   const uint8_t *gw = w + (int64_t)min(n0 + wr, N - 1) * wrow + 16 * ((lane & 1) ^ wswz(wr));
   // scales: wave 0, lane l copies the scale dwords of rows 4 l .. 4 l + 3 (the step's 1 KiB block)
-  const uint8_t *gs = sp + ((int64_t)tn * steps * 256 + 4 * lane) * 4;
+  const uint8_t *gs = sp + ((int64_t)(n0 >> 8) * steps * 256 + 4 * lane) * 4;
   const bool sw = wave == 0;
   auto issue = [&](int s) __attribute__((always_inline)) {
-    const uint32_t st = lds0 + (uint32_t)((s % V_STAGES) * V_STAGE);
+    const uint32_t st = lds0 + (uint32_t)((s % V_STAGES) * G::STAGE);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) gp_dma16(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
-    gp_dma16(gw + s * 32, st + V_ATILE + wave * 1024);
-    if (sw) gp_dma16(gs + s * 1024, st + V_ATILE + V_WTILE);
+    for (int i = 0; i < FI; ++i) gp_dma16(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
+    gp_dma16(gw + s * 32, st + G::ATILE + wave * 1024);
+    if (sw) gp_dma16(gs + s * 1024, st + G::ATILE + V_WTILE);
   };
 
   // fragment geometry (32x32x16 bf16 operands: lane l holds row l % 32 and, in
   // sub-step ks, the step's elements 32 fh + 8 ks + [0, 8) with fh = l / 32:
   // x slot 4 fh + ks, W dword 4 fh + ks)
   const int fr = lane & 31, fh = lane >> 5;
-  int oa[4], ab[4], ob[2], os[2];
+  int oa[FI], ab[FI], ob[2], os[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = wm * 128 + i * 32 + fr;
+  for (int i = 0; i < FI; ++i) {
+    const int r = wm * WM + i * 32 + fr;
     oa[i] = r * 128;
     ab[i] = (4 * fh) ^ aswz(r);  // physical slot of logical slot 4 fh + ks is ks ^ ab
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int r = wn * 64 + j * 32 + fr;
-    ob[j] = V_ATILE + r * 32 + 16 * (fh ^ wswz(r));
-    os[j] = V_ATILE + V_WTILE + r * 4;
+    ob[j] = G::ATILE + r * 32 + 16 * (fh ^ wswz(r));
+    os[j] = G::ATILE + V_WTILE + r * 4;
   }
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[FI][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -141,19 +154,19 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
   // which refills stage k - 1, is issued by both groups in interval 2k + 1
   // (group 0 at the start of its computing interval, group 1 in its loading
   // interval); at the barrier ending interval 2k + 1 every wave waits for its
-  // DMA(k + 1) (only DMA(k + 2), V_DMA_S / V_DMA loads, may remain in flight).
+  // DMA(k + 1) (only DMA(k + 2), DMA_S / DMA loads, may remain in flight).
   const int grp = wave >> 2;
   issue(0);
   if (steps > 1) issue(1);
   if (steps <= 1) gp_wait_barrier<0>();
-  else if (sw) gp_wait_barrier<V_DMA_S>();
-  else gp_wait_barrier<V_DMA>();
+  else if (sw) gp_wait_barrier<G::DMA_S>();
+  else gp_wait_barrier<G::DMA>();
 
   auto pp_step = [&](auto grp_c, auto dma_c, int s) __attribute__((always_inline)) {
     constexpr int GRP = decltype(grp_c)::value;
     constexpr bool DMA = decltype(dma_c)::value;
     if constexpr (DMA && GRP == 1) issue(s + 2);  // interval 2s + 1
-    const uint8_t *st = lds + (s % V_STAGES) * V_STAGE;
+    const uint8_t *st = lds + (s % V_STAGES) * G::STAGE;
     uint4 wq[2];
     uint32_t wsc[2];
 #pragma unroll
@@ -172,42 +185,42 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
         bf[ks][j] = deq8_nvfp4(word, (wsc[j] >> (8 * (2 * fh + (ks >> 1)))) & 0xFF);  // group 2 fh + ks / 2
       }
     // the first sub-step's x fragments too (the stage is complete since the last barrier)
-    bf16x8_t af[2][4];
+    bf16x8_t af[2][FI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[0][i] = *(const bf16x8_t *)(st + oa[i] + 16 * ab[i]);  // ks = 0
+    for (int i = 0; i < FI; ++i) af[0][i] = *(const bf16x8_t *)(st + oa[i] + 16 * ab[i]);  // ks = 0
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (GRP == 0) gp_lds_barrier();
-    else if constexpr (DMA) gp_wait_barrier<V_DMA>();
+    else if constexpr (DMA) gp_wait_barrier<G::DMA>();
     else gp_wait_barrier<0>();
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (DMA && GRP == 0) issue(s + 2);  // interval 2s + 1
     // computing interval: sub-step ks + 1's x fragments are read while sub-step
-    // ks's eight MFMAs run
+    // ks's 2 FI MFMAs run
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       if (ks < 3) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < FI; ++i)
           af[(ks + 1) & 1][i] = *(const bf16x8_t *)(st + oa[i] + 16 * ((ks + 1) ^ ab[i]));
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < FI; ++i)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bf[ks][j], acc[i][j], 0, 0, 0);
     }
     // keep that order: the scheduler would otherwise sink each read next to its use
 #pragma unroll
     for (int ks = 0; ks < 3; ++ks) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // 4 LDS reads (sub-step ks + 1)
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // then sub-step ks's 8 MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, FI, 0);      // FI LDS reads (sub-step ks + 1)
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * FI, 0);  // then sub-step ks's MFMAs
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * FI, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (GRP == 1) gp_lds_barrier();
     else if constexpr (DMA) {
-      if (sw) gp_wait_barrier<V_DMA_S>();
-      else gp_wait_barrier<V_DMA>();
+      if (sw) gp_wait_barrier<G::DMA_S>();
+      else gp_wait_barrier<G::DMA>();
     } else {
       gp_wait_barrier<0>();
     }
@@ -228,11 +241,35 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
   // which no fragment read or DMA is outstanding), in two halves of the wave's 128 rows
   // so that the eight regions fit the ring
   constexpr int REGION = 64 * (64 * 2 + 32);
-  static_assert(8 * REGION <= V_LDS, "the epilogue regions fit the ring");
+  static_assert(8 * REGION <= V_LDS, "the epilogue regions fit the launch's ring");
   const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
   uint8_t *region = lds + wave * REGION;
-  gp_store_tile_bf16<4, 2, 0, 2>(acc, region, lane, y, M, N, m0 + wm * 128, n0 + wn * 64, N, vec);
-  gp_store_tile_bf16<4, 2, 2, 2>(acc, region, lane, y, M, N, m0 + wm * 128, n0 + wn * 64, N, vec);
+  gp_store_tile_bf16<FI, 2, 0, 2>(acc, region, lane, y, M, N, m0 + wm * WM, n0 + wn * 64, n_end, vec);
+  if constexpr (FI == 4)
+    gp_store_tile_bf16<FI, 2, 2, 2>(acc, region, lane, y, M, N, m0 + wm * WM, n0 + wn * 64, n_end, vec);
+}
+
+__global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16_t *__restrict__ x,
+                                                                    const uint8_t *__restrict__ w,
+                                                                    const uint8_t *__restrict__ sp,
+                                                                    uint16_t *__restrict__ y, int M, int N, int K) {
+  nv_tile<256>(blockIdx.x, x, w, sp, y, M, N, K, 0, N);
+}
+
+// Both tile heights in one launch: blocks [0, tiles1) are the 256-row tiles of W rows
+// [0, n_split), the rest the 128-row tiles of W rows [n_split, N).  Blocks start in
+// index order as CUs free up, so a partial last round of 256-row tiles runs as twice as
+// many half tiles, each moving 25 of the 41 KiB a full tile moves per K step.
+__global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_split_kernel(const uint16_t *__restrict__ x,
+                                                                          const uint8_t *__restrict__ w,
+                                                                          const uint8_t *__restrict__ sp,
+                                                                          uint16_t *__restrict__ y, int M, int N,
+                                                                          int K, int n_split, int tiles1) {
+  const int b = blockIdx.x;
+  if (b < tiles1)
+    nv_tile<256>(b, x, w, sp, y, M, N, K, 0, n_split);
+  else
+    nv_tile<128>(b - tiles1, x, w, sp, y, M, N, K, n_split, N);
 }
 
 static size_t round256v(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -256,12 +293,27 @@ hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
     if (e != hipSuccess) return e;
     tiled = (const uint8_t *)ws;
   }
-  static std::atomic<uint64_t> lds_set{0};
+  static std::atomic<uint64_t> lds_set{0}, lds_split{0};
   e = ensure_dynamic_lds(lds_set, (const void *)gemm_nvfp4_pipe_kernel, (int)V_LDS);
+  if (e == hipSuccess) e = ensure_dynamic_lds(lds_split, (const void *)gemm_nvfp4_pipe_split_kernel, (int)V_LDS);
   if (e != hipSuccess) return e;
-  const int tiles = ((a.M + V_BM - 1) / V_BM) * ((a.N + V_BN - 1) / V_BN);
-  hipLaunchKernelGGL(gemm_nvfp4_pipe_kernel, dim3(tiles), dim3(V_THREADS), V_LDS, st, (const uint16_t *)a.x, a.w,
-                     tiled, (uint16_t *)a.y, a.M, a.N, a.K);
+  // When the 256 x 256 tiles leave a partial last round of whole tile-columns that half
+  // the CUs or fewer would run, those columns run as 128 x 256 tiles in the same launch.
+  const int tiles_m = (a.M + V_BM - 1) / V_BM, tiles_n = (a.N + V_BN - 1) / V_BN;
+  const int cus = device_cu_count();
+  const int rem = cus > 0 ? (tiles_m * tiles_n) % cus : 0;
+  int n_split = a.N;
+  if (rem != 0 && rem % tiles_m == 0 && 2 * rem <= cus && tiles_m * tiles_n > cus)
+    n_split = (tiles_n - rem / tiles_m) * V_BN;
+  const int tiles1 = tiles_m * ((n_split + V_BN - 1) / V_BN);
+  if (n_split == a.N) {
+    hipLaunchKernelGGL(gemm_nvfp4_pipe_kernel, dim3(tiles1), dim3(V_THREADS), V_LDS, st, (const uint16_t *)a.x, a.w,
+                       tiled, (uint16_t *)a.y, a.M, a.N, a.K);
+    return hipGetLastError();
+  }
+  const int tiles2 = ((a.M + 127) / 128) * ((a.N - n_split + V_BN - 1) / V_BN);
+  hipLaunchKernelGGL(gemm_nvfp4_pipe_split_kernel, dim3(tiles1 + tiles2), dim3(V_THREADS), V_LDS, st,
+                     (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, n_split, tiles1);
   return hipGetLastError();
 }
 

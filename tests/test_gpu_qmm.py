@@ -664,13 +664,16 @@ def test_random_shapes_match_oracle():
     torch.cuda.synchronize()
 
 
-# mxfp8 prefill shapes whose 256 x 256 tiles leave a partial last round that whole W
-# tile-columns fill: those columns run as 128 x 128 tiles in the same launch.  M = 2000
-# (8 row tiles, the last one ragged) with N = 8448 (33 tile-columns: 264 tiles, 8 left
-# over = one column) and N = 8704 (34 columns: 272 tiles, 16 left over = two columns).
-@pytest.mark.parametrize("M,N", [(2000, 8448), (2048, 8704)])
-def test_prefill_with_tail_tiles_in_one_launch(M, N):
-    mode, K = "mxfp8", 640
+# Prefill shapes whose 256 x 256 tiles leave a partial last round that whole W
+# tile-columns fill: those columns run as smaller tiles in the same launch (mxfp8:
+# 128 x 128, nvfp4: 128 x rows of x by 256 W rows).  M = 2000 (8 row tiles, the last one
+# ragged) with N = 8448 (33 tile-columns: 264 tiles, 8 left over = one column), N = 8348
+# (the same with a ragged last column) and N = 8704 (34 columns: 272 tiles, 16 left
+# over = two columns).
+@pytest.mark.parametrize("mode,M,N", [("mxfp8", 2000, 8448), ("mxfp8", 2048, 8704), ("nvfp4", 2000, 8348),
+                                      ("nvfp4", 2048, 8704)])
+def test_prefill_with_tail_tiles_in_one_launch(mode, M, N):
+    K = 640
     rng = np.random.default_rng(M + N)
     wq, s = rand_w(rng, mode, N, K)
     xb = make_x(rng, M, K, "edge")
