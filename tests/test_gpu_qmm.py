@@ -669,9 +669,11 @@ def test_random_shapes_match_oracle():
 # 128 x 128, nvfp4: 128 x rows of x by 256 W rows).  M = 2000 (8 row tiles, the last one
 # ragged) with N = 8448 (33 tile-columns: 264 tiles, 8 left over = one column), N = 8348
 # (the same with a ragged last column) and N = 8704 (34 columns: 272 tiles, 16 left
-# over = two columns).
+# over = two columns).  nvfp4 with one row tile: M = 100 and 200, N = 76800 (300 tiles,
+# 44 left over: one 128-row tail tile per column at M = 100, two at M = 200, the second
+# ragged).
 @pytest.mark.parametrize("mode,M,N", [("mxfp8", 2000, 8448), ("mxfp8", 2048, 8704), ("nvfp4", 2000, 8348),
-                                      ("nvfp4", 2048, 8704)])
+                                      ("nvfp4", 2048, 8704), ("nvfp4", 100, 76800), ("nvfp4", 200, 76800)])
 def test_prefill_with_tail_tiles_in_one_launch(mode, M, N):
     K = 640
     rng = np.random.default_rng(M + N)
