@@ -89,7 +89,16 @@ int qmm_synchronize(qmm_stream s);                /* mlx_synchronize */
  * new array.  Prefill calls (M > 8) read the scales in a tile-major copy that the
  * library makes at the first such call with this scales handle (not while the
  * stream is being captured) and frees with the handle: as with mlx arrays, the
- * contents behind a handle must not change while it lives. */
+ * contents behind a handle must not change while it lives.  The copy holds
+ * round_up(N, 256) * K / group bytes of device memory (1/8 of the packed weight
+ * bytes for nvfp4, 1/32 for mxfp8).  It is complete on the device before any call
+ * uses it: the first prefill call with a handle waits for its stream once, after
+ * which calls on any stream or thread read the copy with no further ordering.
+ * Freeing a handle that holds a copy waits for the device (hipFree).
+ * Prefill calls also take per-call scratch from a workspace kept per device and
+ * stream (see qmm_gdn_recurrence); a graph captured on a stream uses that stream's
+ * workspace when it is large enough, so replays of it must not overlap eager calls
+ * on the capture stream (replay on that stream, or synchronize in between). */
 int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array scales, qmm_array biases,
                          bool transpose_w, qmm_optional_int group_size, qmm_optional_int bits,
                          const char *mode, qmm_stream s);
@@ -213,6 +222,9 @@ bool qmm_fault_did_fire(void);
 uint64_t qmm_op_count(void);
 /* Grouped calls (qmm_quantized_matmul_group) that ran as one kernel launch (diagnostics). */
 uint64_t qmm_group_launch_count(void);
+/* Bytes of device memory held by the tile-major scale copies of live scales handles
+ * (see qmm_quantized_matmul; diagnostics, no mlx-c counterpart). */
+uint64_t qmm_scale_copy_bytes(void);
 
 /* ---- weights (src/weights.zig) ---- */
 typedef enum { QMM_QUANT_NONE = 0, QMM_QUANT_MXFP8 = 1, QMM_QUANT_NVFP4 = 2 } qmm_quant_mode;

@@ -242,10 +242,24 @@ int alloc_arr(qmm_array *res, const std::vector<int> &shape, qmm_dtype dtype, hi
   return 0;
 }
 
+// Bytes held by the tile-major scale copies of live handles (diagnostics).
+static std::atomic<uint64_t> g_tiled_bytes{0};
+
+void release_tiled(Arr *a) {
+  if (!a || !a->tiled) return;
+  // A plain allocation: hipFree waits for the device first, so work already queued on any
+  // stream that reads the copy completes before it goes; no caller stream is involved.
+  (void)hipFree(a->tiled);
+  (void)hipGetLastError();
+  g_tiled_bytes.fetch_sub(a->tiled_bytes, std::memory_order_relaxed);
+  a->tiled = nullptr;
+  a->tiled_bytes = 0;
+}
+
 void release_arr(Arr *a) {
   if (!a) return;
   if (a->owned && a->data) (void)hipFreeAsync(a->data, a->alloc_stream);
-  if (a->tiled) (void)hipFreeAsync(a->tiled, a->tiled_stream);
+  release_tiled(a);
   delete a;
 }
 
@@ -416,10 +430,13 @@ static int consume_latch() {
 // waits for the device: errors of work still in flight surface at the call that waits
 // for it (qmm_synchronize, qmm_array_to_host), which latches them.
 // Without a device the runtime answers every call with hipErrorNoDevice: that is no
-// work's error (an op that needs the device reports it itself).
+// work's error (an op that needs the device reports it itself).  hipErrorNotReady is the
+// answer of a query (hipStreamQuery, hipEventQuery) whose work has not finished yet, which
+// the caller's own polling leaves behind: a status, not a failure.
 static void latch_runtime_error() {
   const hipError_t e = hipGetLastError();
-  if (e != hipSuccess && e != hipErrorNoDevice) fail_hip(e, "qmm_check_error: pending HIP runtime error");
+  if (e != hipSuccess && e != hipErrorNoDevice && e != hipErrorNotReady)
+    fail_hip(e, "qmm_check_error: pending HIP runtime error");
 }
 int qmm_check_error(void) {
   latch_runtime_error();
@@ -502,36 +519,48 @@ static int check_wq(const Arr *w, const Arr *sc, int mode, const char *op, int *
 
 // The scales of `sa` in the prefill GEMMs' tile-major layout, made once per handle and kept
 // with it: mlx arrays are immutable, so the contents behind a handle do not change while it
-// lives.  Null when the GEMM for `a` reads the scales as stored, while the stream is being
-// captured and no copy exists yet (it would become part of the graph), or if the copy
-// cannot be made; the GEMM then repacks into its workspace on every call.
+// lives.  *out is null when the GEMM for `a` reads the scales as stored, while the stream is
+// being captured and no copy exists yet (it would become part of the graph), or if the copy
+// cannot be allocated; the GEMM then repacks into its workspace on every call.
+//
+// The copy is published only once it is complete on the device: a plain allocation (not
+// stream-ordered), the repack on the caller's stream, then a wait for that stream.  A call
+// on any other stream or thread that finds the pointer can read it with no further
+// ordering, and freeing it (release_tiled) does not need the stream that made it.  The
+// wait happens once per handle, at its first prefill call.  Returns non-zero, with the
+// error latched, only when the stream reports a device error.
 static std::mutex g_tiled_mtx;
-static const uint32_t *tiled_scales(Arr *sa, const QmmArgs &a, hipStream_t st) {
+static int tiled_scales(Arr *sa, const QmmArgs &a, hipStream_t st, const uint32_t **out) {
+  *out = nullptr;
   const int nb = gemm_tiled_scale_bytes_per_row(a);
-  if (!nb || !sa || sa->ndim != 2 || sa->shape[0] != a.N || sa->shape[1] != nb) return nullptr;
+  if (!nb || !sa || sa->ndim != 2 || sa->shape[0] != a.N || sa->shape[1] != nb) return 0;
   std::lock_guard<std::mutex> lk(g_tiled_mtx);
-  if (sa->tiled && sa->tiled_nb == nb) return (const uint32_t *)sa->tiled;
+  if (sa->tiled) {  // nb is the handle's own row length, so an existing copy always fits
+    *out = (const uint32_t *)sa->tiled;
+    return 0;
+  }
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
     (void)hipGetLastError();
-    return nullptr;
+    return 0;
   }
-  pool_init();
+  const size_t bytes = tiled_scales_bytes(a.N, nb);
   void *p = nullptr;
-  if (hipMallocAsync(&p, tiled_scales_bytes(a.N, nb), st) != hipSuccess) {
+  if (hipMalloc(&p, bytes) != hipSuccess) {
     (void)hipGetLastError();
-    return nullptr;
+    return 0;
   }
-  if (launch_repack_scales(a.s, (int64_t)a.N, nb, (uint32_t *)p, st) != hipSuccess) {
-    (void)hipGetLastError();
-    (void)hipFreeAsync(p, st);
-    return nullptr;
+  hipError_t e = launch_repack_scales(a.s, (int64_t)a.N, nb, (uint32_t *)p, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return fail_hip(e, "qmm::tiled_scales");
   }
-  if (sa->tiled) (void)hipFreeAsync(sa->tiled, sa->tiled_stream);
   sa->tiled = p;
-  sa->tiled_nb = nb;
-  sa->tiled_stream = st;
-  return (const uint32_t *)p;
+  sa->tiled_bytes = bytes;
+  g_tiled_bytes.fetch_add(bytes, std::memory_order_relaxed);
+  *out = (const uint32_t *)p;
+  return 0;
 }
 
 // Workspace bytes run_qmm needs for these arguments (0 for the decode kernels).
@@ -559,7 +588,7 @@ static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op, vo
       e = (aligned && qmv_fast_ok(a)) ? launch_qmv(a, st) : launch_qmv_generic(a, st);
   } else if (aligned && (gemm_mxfp8_ok(a) || gemm_nvfp4_ok(a))) {
     const bool fp8 = gemm_mxfp8_ok(a);
-    if (!a.s_tiled) a.s_tiled = tiled_scales(scales_arr, a, st);
+    if (!a.s_tiled && tiled_scales(scales_arr, a, st, &a.s_tiled)) return 1;
     const size_t need = fp8 ? gemm_mxfp8_workspace(a) : gemm_nvfp4_workspace(a);
     void *ws = ws_given;
     bool transient = false;
@@ -634,6 +663,7 @@ int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array sca
 // its own result.
 static std::atomic<uint64_t> g_group_launches{0};
 uint64_t qmm_group_launch_count(void) { return g_group_launches.load(std::memory_order_relaxed); }
+uint64_t qmm_scale_copy_bytes(void) { return g_tiled_bytes.load(std::memory_order_relaxed); }
 
 int qmm_quantized_matmul_group(qmm_array *res, size_t n, qmm_array x, const qmm_array *w, const qmm_array *scales,
                                qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
@@ -923,8 +953,8 @@ int qmm_mlp_gate_up_silu(qmm_array *res, qmm_array x, qmm_array w_gate, qmm_arra
   QmmArgs b = a;
   b.w = wu;
   b.s = su;
-  a.s_tiled = tiled_scales((Arr *)s_gate.ctx, a, st);
-  b.s_tiled = tiled_scales((Arr *)s_up.ctx, b, st);
+  if (tiled_scales((Arr *)s_gate.ctx, a, st, &a.s_tiled) || tiled_scales((Arr *)s_up.ctx, b, st, &b.s_tiled))
+    return finish(1);
   const size_t gemm_ws = std::max(qmm_workspace(a), qmm_workspace(b));
   void *ws = nullptr;
   bool transient = false;

@@ -21,11 +21,11 @@ struct Arr {
   int ndim = 0;
   int shape[QMM_MAX_DIM] = {0};
   qmm_dtype dtype = QMM_BOOL;
-  // For a scales array: a copy in the prefill GEMMs' tile-major layout, made at the first
-  // prefill call that reads it and freed with the handle (tiled_nb scale bytes per row).
+  // For a scales array: a copy in the prefill GEMMs' tile-major layout (tiled_bytes bytes,
+  // a plain allocation), made at the first prefill call that reads it, complete on the
+  // device before it is set, and freed with the handle (release_tiled).
   void *tiled = nullptr;
-  int tiled_nb = 0;
-  hipStream_t tiled_stream = nullptr;
+  size_t tiled_bytes = 0;
   size_t size() const;
   size_t nbytes() const { return size() * dtype_size(dtype); }
 };
@@ -50,6 +50,8 @@ int workspace(hipStream_t st, size_t bytes, void **out, bool *transient);
 Arr *new_arr(const int *shape, int dim, qmm_dtype dtype);
 int alloc_arr(qmm_array *res, const std::vector<int> &shape, qmm_dtype dtype, hipStream_t st, Arr **out);
 void release_arr(Arr *a);
+// Frees the handle's tile-major scale copy, if it has one (waits for the device first).
+void release_tiled(Arr *a);
 hipStream_t stream_of(qmm_stream s);
 
 }  // namespace qmm

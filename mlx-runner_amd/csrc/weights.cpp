@@ -30,7 +30,10 @@ struct WeightMap {
   std::vector<void *> buffers;  // hipMalloc'd tensor buffers
   qmm_quant_spec quant{QMM_QUANT_NONE, 0, 0};
   ~WeightMap() {
-    for (auto &kv : map) delete kv.second;  // buffers freed below
+    for (auto &kv : map) {  // the tensor buffers are freed below; a scales handle's tile-major copy here
+      release_tiled(kv.second);
+      delete kv.second;
+    }
     for (void *b : buffers) (void)hipFree(b);
   }
 };

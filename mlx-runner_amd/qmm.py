@@ -112,6 +112,7 @@ _SIGS = {
     "qmm_fault_did_fire": (c_bool, []),
     "qmm_op_count": (c_uint64, []),
     "qmm_group_launch_count": (c_uint64, []),
+    "qmm_scale_copy_bytes": (c_uint64, []),
     "qmm_infer_quant_spec_json": (c_int, [c_char_p, c_size_t, POINTER(qmm_quant_spec), POINTER(c_size_t)]),
     "qmm_parse_header_json": (c_int, [c_char_p, c_size_t, POINTER(c_size_t)]),
     "qmm_sanitize_name": (c_int, [c_char_p, c_char_p, c_size_t]),
