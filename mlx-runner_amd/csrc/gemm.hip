@@ -7,8 +7,14 @@
 // Tiling (gfx950, wave64, 256 threads):
 //   block tile 128 (x rows) x 128 (W rows), K step 32;
 //   each thread stages 16 elements of one x row and 16 of one W row into LDS;
-//   W elements are unpacked with the gfx950 converters and scaled in f32 (exact:
-//   every nvfp4 / in-range mxfp8 value is exact in bf16), so LDS holds bf16;
+//   W elements are unpacked with the gfx950 converters, so LDS holds bf16:
+//     nvfp4: E2M1 times its E4M3 scale in f32, exact in bf16 (at most 6
+//            significant bits, magnitudes 2^-10 .. 2688);
+//     mxfp8: the E4M3 codes unscaled (exact in bf16).  A K step is one 32-element
+//            scale block, so each step's MFMA sums go to a temporary and are added
+//            to the accumulator times the W row's E8M0 scale in f32: a weight whose
+//            f32 (or bf16) dequant would overflow or underflow still multiplies x
+//            as its true value, as in the other kernels;
 //   4 waves in 2x2, each owning 64x64 of the tile as 2x2 v_mfma_f32_32x32x16_bf16
 //   accumulators (fp32); epilogue rounds to bf16 (RNE).
 #include "qmm_device.h"
@@ -26,19 +32,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return (uint32_t)f32_to_bf16_rne(a) | ((uint32_t)f32_to_bf16_rne(b) << 16);
 }
 
-// 16 consecutive W elements of row n starting at k (k a multiple of 16) as 8 bf16 pairs.
+// 16 consecutive W elements of row n starting at k (k a multiple of 16) as 8 bf16 pairs
+// (mxfp8: unscaled codes, the block's scale in *sc_out; otherwise dequantized).
 template <int MODE>
 __device__ __forceinline__ void load_w16(const uint8_t *__restrict__ w, const uint8_t *__restrict__ s, int64_t n,
-                                         int k, int K, uint32_t out[8]) {
+                                         int k, int K, uint32_t out[8], float *sc_out) {
   if constexpr (MODE == MXFP8) {
     const uint4 q = *(const uint4 *)(w + n * (int64_t)K + k);
-    const float sc = e8m0_to_f32(s[n * (int64_t)(K >> 5) + (k >> 5)]);
+    *sc_out = e8m0_to_f32(s[n * (int64_t)(K >> 5) + (k >> 5)]);
     const uint32_t d[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      f32x2_t a = fp8x2_to_f32x2<false>(d[j]), b = fp8x2_to_f32x2<true>(d[j]);
-      out[2 * j] = pack_bf16x2(a.x * sc, a.y * sc);
-      out[2 * j + 1] = pack_bf16x2(b.x * sc, b.y * sc);
+      out[2 * j] = __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<false>(d[j]));
+      out[2 * j + 1] = __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<true>(d[j]));
     }
   } else if constexpr (MODE == NVFP4) {
     const uint2 q = *(const uint2 *)(w + n * (int64_t)(K >> 1) + (k >> 1));
@@ -67,6 +73,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t *__restri
                                                         int N, int K) {
   __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDK];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[BN * LDK];
+  __shared__ float Ss[MODE == MXFP8 ? BN : 1];  // mxfp8: the step's scale of each W row
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
@@ -90,15 +97,27 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t *__restri
       a1 = p[1];
     }
     uint32_t b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float sc = 0.f;
     const int n = n0 + lrow;
-    if (n < N && kk < K) load_w16<MODE>(w, s, n, kk, K, b);
+    if (n < N && kk < K) load_w16<MODE>(w, s, n, kk, K, b, &sc);
     uint4 *ad = (uint4 *)(As + lrow * LDK + 16 * lh);
     ad[0] = a0;
     ad[1] = a1;
     uint4 *bd = (uint4 *)(Bs + lrow * LDK + 16 * lh);
     bd[0] = make_uint4(b[0], b[1], b[2], b[3]);
     bd[1] = make_uint4(b[4], b[5], b[6], b[7]);
+    if constexpr (MODE == MXFP8)
+      if (lh == 0) Ss[lrow] = sc;  // both halves of a row's step are one 32-block
     __syncthreads();
+    f32x16_t part[2][2];
+    if constexpr (MODE == MXFP8) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) part[i][j][v] = 0.f;
+    }
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       bf16x8_t af[2], bf[2];
@@ -111,7 +130,23 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t *__restri
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) {
+          if constexpr (MODE == MXFP8)
+            part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], part[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    if constexpr (MODE == MXFP8) {
+      // accumulator column = W row wn * 64 + j * 32 + lane % 32 of the tile
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float scj = Ss[wn * 64 + j * 32 + (lane & 31)];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[i][j][v] = __builtin_fmaf(part[i][j][v], scj, acc[i][j][v]);
+      }
     }
     __syncthreads();
   }

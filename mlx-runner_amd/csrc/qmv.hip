@@ -176,7 +176,10 @@ __global__ __launch_bounds__(64) void qmv_kernel(const void *__restrict__ xv, co
 }
 
 // Any-shape fallback (K a multiple of the group, row bytes not a multiple of 16):
-// one wave per (row, m), lanes stride elements; exact integer decoders.
+// one wave per (row, m), lanes stride elements; exact integer decoders.  Each term
+// is (x * elem) * scale in one fused step, so a weight whose f32 dequant would
+// overflow still multiplies x as its true value (0 * it is 0), as in the other
+// kernels, which scale each group's partial sum.
 template <int MODE, bool XF32>
 __global__ __launch_bounds__(64) void qmv_generic_kernel(const void *__restrict__ xv, const uint8_t *__restrict__ w,
                                                          const uint8_t *__restrict__ s, void *__restrict__ yv,
@@ -197,7 +200,7 @@ __global__ __launch_bounds__(64) void qmv_generic_kernel(const void *__restrict_
       sc = e4m3_to_f32_int(sr[k >> 4]);
     }
     float xk = XF32 ? ((const float *)xv)[(int64_t)m * K + k] : bf16_to_f32(((const uint16_t *)xv)[(int64_t)m * K + k]);
-    acc = __builtin_fmaf(xk, e * sc, acc);
+    acc = __builtin_fmaf(xk * e, sc, acc);
   }
   acc = wave_sum(acc);
   if (lane == 0) {

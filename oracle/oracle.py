@@ -56,6 +56,7 @@ def lib():
             ("oracle_e2m1_encode", u8, [f64]),
             ("oracle_dequant", None, [i32, vp, vp, i64, i64, vp]),
             ("oracle_dequant_bf16", None, [i32, vp, vp, i64, i64, vp]),
+            ("oracle_dequant_f64", None, [i32, vp, vp, i64, i64, vp]),
             ("oracle_quantize", None, [i32, vp, i64, i64, vp, vp]),
             ("oracle_qmm", i32, [i32, i32, vp, i64, i64, vp, vp, i64, vp, i64, i32, vp, i32, i32]),
         ]:
@@ -123,6 +124,16 @@ def dequant(mode: str, w: np.ndarray, s: np.ndarray, K: int) -> np.ndarray:
     return out
 
 
+def dequant_f64(mode: str, w: np.ndarray, s: np.ndarray, K: int) -> np.ndarray:
+    """The exact dequantized weights (elem * scale in float64; never overflows)."""
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    s = np.ascontiguousarray(s, dtype=np.uint8)
+    N = w.shape[0]
+    out = np.empty((N, K), dtype=np.float64)
+    lib().oracle_dequant_f64(MODES[mode], _ptr(w), _ptr(s), N, K, _ptr(out))
+    return out
+
+
 def dequant_bf16(mode: str, w: np.ndarray, s: np.ndarray, K: int) -> np.ndarray:
     w = np.ascontiguousarray(w, dtype=np.uint32)
     s = np.ascontiguousarray(s, dtype=np.uint8)
@@ -152,7 +163,9 @@ def qmm(mode: str, x: np.ndarray, w: np.ndarray, s: np.ndarray, *, x_is_bf16: bo
     x: [M, K] as bf16 bits (uint16, ``x_is_bf16``) or float32.
     cols: optional output-column subset (int64 indices into N).
     out: "bf16" (uint16 bits, RNE of the double sum) or "f32".
-    f32acc: fp32 accumulation (the CPU-baseline form) instead of double.
+    f32acc: f32 weights and fp32 accumulation (the CPU-baseline form) instead of
+    exact weights and a double sum (the parity form: a weight is elem * scale
+    exactly, NaN codes and scales make it NaN, and only the final sum rounds).
     """
     x = np.ascontiguousarray(x, dtype=np.uint16 if x_is_bf16 else np.float32)
     w = np.ascontiguousarray(w, dtype=np.uint32)

@@ -29,6 +29,15 @@
  *     E4M3 saturating at 448); nvfp4 scale = RNE_E4M3(amax / 6), elements
  *     RNE (ties to even code) to E2M1 of x / scale, saturating at 6.  Every
  *     rounding decision is made by exact comparisons.
+ *   - Special values in quantized_matmul (assumption, unpinned): the
+ *     dequantized weight elem * scale is taken exactly (double holds every
+ *     product, 448 * 2^127 included), so a weight whose f32 dequant would
+ *     overflow still multiplies x as its true value (0 * it is 0, and a tiny x
+ *     gives a finite result); a NaN element code (E4M3 S.1111.111) or a NaN
+ *     scale (E8M0 0xFF, E4M3 S.1111.111) makes the weight NaN and so every
+ *     output that sums over it; y is the exact sum rounded once to bf16
+ *     (overflow to +-inf).  mlx_dequantize to f32 rounds the same exact value
+ *     to f32 (overflow to +-inf).
  *
  * Build: see oracle/Makefile (gcc -O3, pthreads).  No GPU, no torch.
  */
@@ -130,6 +139,17 @@ void oracle_dequant(int mode, const uint32_t *w, const uint8_t *s, int64_t N, in
       double v = (double)elem_value(mode, elem_code(mode, row, k)) * (double)scale_value(mode, s[n * spr + k / g]);
       out[n * K + k] = f64_to_f32(v);
     }
+  }
+}
+
+/* w[n,k] = elem(code) * scale exactly, in double (no overflow: |w| <= 448 * 2^127). */
+void oracle_dequant_f64(int mode, const uint32_t *w, const uint8_t *s, int64_t N, int64_t K, double *out) {
+  int g = group_of(mode);
+  int64_t wpr = words_per_row(mode, K), spr = K / g;
+  for (int64_t n = 0; n < N; ++n) {
+    const uint32_t *row = w + n * wpr;
+    for (int64_t k = 0; k < K; ++k)
+      out[n * K + k] = (double)elem_value(mode, elem_code(mode, row, k)) * (double)scale_value(mode, s[n * spr + k / g]);
   }
 }
 
@@ -308,6 +328,19 @@ static void build_tables(void) {
   for (int i = 0; i < 16; ++i) T_E2M1[i] = oracle_e2m1_to_f32((uint8_t)i);
 }
 
+/* The exact weights of one row (the parity path): every product of an element
+ * and a scale is exact in double. */
+static void dequant_row_f64(int mode, const uint32_t *row, const uint8_t *srow, int64_t K, double *out) {
+  if (mode == QMM_MODE_MXFP8) {
+    for (int64_t k = 0; k < K; ++k)
+      out[k] = (double)T_E4M3[(row[k >> 2] >> (8 * (k & 3))) & 0xFF] * (double)T_E8M0[srow[k >> 5]];
+  } else {
+    for (int64_t k = 0; k < K; ++k)
+      out[k] = (double)T_E2M1[(row[k >> 3] >> (4 * (k & 7))) & 0xF] * (double)T_E4M3[srow[k >> 4]];
+  }
+}
+
+/* f32 weights (the CPU-baseline form): each product rounded once to f32. */
 static void dequant_row_f32(int mode, const uint32_t *row, const uint8_t *srow, int64_t K, float *out) {
   if (mode == QMM_MODE_MXFP8) {
     for (int64_t k = 0; k < K; ++k) out[k] = T_E4M3[(row[k >> 2] >> (8 * (k & 3))) & 0xFF] * T_E8M0[srow[k >> 5]];
@@ -321,9 +354,13 @@ static void *qmm_worker(void *arg) {
   int g = group_of(j->mode);
   int64_t K = j->K, wpr = words_per_row(j->mode, K), spr = K / g;
   float *drow = (float *)malloc(sizeof(float) * (K + 16));
+  double *ddrow = (double *)malloc(sizeof(double) * (K + 16));
   for (int64_t c = j->c0; c < j->c1; ++c) {
     int64_t n = j->cols ? j->cols[c] : c;
-    dequant_row_f32(j->mode, j->w + n * wpr, j->s + n * spr, K, drow);
+    if (j->f32acc)
+      dequant_row_f32(j->mode, j->w + n * wpr, j->s + n * spr, K, drow);
+    else
+      dequant_row_f64(j->mode, j->w + n * wpr, j->s + n * spr, K, ddrow);
     for (int64_t m = 0; m < j->M; ++m) {
       double acc;
       if (j->f32acc) {
@@ -339,10 +376,11 @@ static void *qmm_worker(void *arg) {
         for (int i = 0; i < 16; ++i) a += part[i];
         acc = (double)a;
       } else {
-        /* products are exact in double (<= 30 significant bits); sum in double. */
+        /* products of x (<= 24 significant bits) and an exact weight (<= 8) are
+         * exact in double; sum in double. */
         const double *xr = j->xd + m * K;
         acc = 0.0;
-        for (int64_t k = 0; k < K; ++k) acc += xr[k] * (double)drow[k];
+        for (int64_t k = 0; k < K; ++k) acc += xr[k] * ddrow[k];
       }
       if (j->out_kind == OUT_BF16)
         ((uint16_t *)j->y)[m * j->ncols + c] = oracle_f64_to_bf16(acc);
@@ -351,13 +389,14 @@ static void *qmm_worker(void *arg) {
     }
   }
   free(drow);
+  free(ddrow);
   return NULL;
 }
 
 /*
  * y[m, c] = sum_k x[m,k] * deq(W)[cols[c], k]  for c < ncols (cols == NULL: all N).
- * f32acc = 0: double accumulation rounded once (the parity oracle).
- * f32acc = 1: fp32 accumulation in K order (the CPU baseline).
+ * f32acc = 0: exact weights, double accumulation rounded once (the parity oracle).
+ * f32acc = 1: f32 weights, fp32 accumulation in K order (the CPU baseline).
  * threads: worker threads splitting the output columns.
  */
 int oracle_qmm(int mode, int x_dtype, const void *x, int64_t M, int64_t K, const uint32_t *w, const uint8_t *s,

@@ -262,6 +262,79 @@ def test_qmm_matches_float64_blas(oracle, mode, M, N, K):
     assert ok, (fro, worst)
 
 
+def test_qmm_special_weights_closed_forms(oracle):
+    """The special-value semantics of the parity oracle, each case a closed form: an
+    mxfp8 weight 448 * 2^(X-127) whose f32 dequant overflows multiplies x exactly
+    (x = 2^-10 gives 1.75 * 2^(X-129); x = 0 gives 0); x = +-1.5 against it overflows
+    to +-inf from X = 247; a NaN scale or NaN element code makes the output NaN even against x = 0;
+    nvfp4 scale 0x01 (2^-9) and 0 are exact, 0x7F / 0xFF are NaN."""
+    K = 64
+    for X in (240, 247, 254):
+        codes = np.zeros(K, np.uint8)
+        codes[5] = 0x7E
+        wq = codes.view(np.uint32).reshape(1, K // 4)
+        s = np.full((1, K // 32), X, np.uint8)
+        assert np.isinf(oracle.dequant("mxfp8", wq, s, K)[0, 5]) == (X >= 247)
+        x = np.zeros((4, K), np.float32)
+        x[0, 5], x[1, 5], x[2, 5], x[3, 5] = 2.0 ** -10, 0.0, 1.5, -1.5
+        y = O.bf16_bits_to_f32(oracle.qmm("mxfp8", O.f32_to_bf16_bits(x), wq, s)).astype(np.float64)
+        assert y[0, 0] == 1.75 * 2.0 ** (X - 129) and y[1, 0] == 0.0
+        big = np.inf if X >= 247 else 1.5 * 448.0 * 2.0 ** (X - 127)  # exact in bf16 below overflow
+        assert y[2, 0] == big and y[3, 0] == -big
+    x = O.f32_to_bf16_bits(np.zeros((1, K), np.float32))
+    for code, sb in ((0x7F, 127), (0xFF, 127), (0x00, 0xFF)):
+        codes = np.zeros(K, np.uint8)
+        codes[40] = code
+        y = oracle.qmm("mxfp8", x, codes.view(np.uint32).reshape(1, K // 4), np.array([[127, sb]], np.uint8))
+        assert np.isnan(O.bf16_bits_to_f32(y)).all(), (code, sb)
+    nib = np.zeros((1, K // 8), np.uint32)
+    nib[0, 0] = 0x7  # element 0 = 6.0
+    xo = np.zeros((1, K), np.float32)
+    xo[0, 0] = 1.0
+    for sb, want in ((0x01, 6.0 * 2.0 ** -9), (0x00, 0.0), (0x7F, np.nan), (0xFF, np.nan)):
+        s = np.full((1, K // 16), 0x38, np.uint8)
+        s[0, 0] = sb
+        y = O.bf16_bits_to_f32(oracle.qmm("nvfp4", O.f32_to_bf16_bits(xo), nib, s))[0, 0]
+        assert (np.isnan(y) and np.isnan(want)) or y == want, (sb, y)
+
+
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+def test_qmm_special_weights_match_torch_tables(oracle, mode):
+    """Every scale byte (NaN included) and every element code (NaN codes included) on random
+    rows, against an independent product: torch's float8_e4m3fn / float8_e8m0fnu tables in
+    float64 (exact products, no f32 dequant), a float64 matmul, one rounding to bf16."""
+    rng = np.random.default_rng(31)
+    N, K, M = 512, 256, 3
+    g = 32 if mode == "mxfp8" else 16
+    e4 = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).double().numpy()
+    e8 = torch.arange(256, dtype=torch.uint8).view(torch.float8_e8m0fnu).double().numpy()
+    e2 = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0.0, -.5, -1, -1.5, -2, -3, -4, -6])
+    if mode == "mxfp8":
+        c = rng.integers(0, 256, size=(N, K), dtype=np.uint8)
+        c[: N // 2] &= 0xF7  # no NaN code in the first half (S.1111.111 needs bit 3)
+        s = np.repeat(rng.integers(0, 256, size=(N, 1), dtype=np.uint8), K // g, axis=1)
+        s[: N // 2] = np.arange(N // 2)[:, None] % 255  # every non-NaN byte, one per row
+        wq = np.ascontiguousarray(c).view(np.uint32).reshape(N, K // 4)
+        D = e4[c] * np.repeat(e8[s], g, axis=1)
+    else:
+        c = rng.integers(0, 16, size=(N, K), dtype=np.uint32)
+        s = rng.integers(0, 256, size=(N, K // g), dtype=np.uint8)
+        s[: N // 2] = (np.arange(N // 2)[:, None] + np.arange(K // g)[None, :]) % 127
+        wq = np.zeros((N, K // 8), np.uint32)
+        for i in range(8):
+            wq |= c[:, i::8] << np.uint32(4 * i)
+        D = e2[c] * np.repeat(e4[s], g, axis=1)
+    xb = O.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = O.bf16_bits_to_f32(xb).astype(np.float64) @ D.T
+    y = O.bf16_bits_to_f32(oracle.qmm(mode, xb, wq, s)).astype(np.float64)
+    assert np.isnan(ref).any() and np.isfinite(ref).any()
+    assert np.array_equal(np.isnan(y), np.isnan(ref))
+    fin = np.isfinite(ref)
+    assert np.array_equal(y[fin], O.bf16_bits_to_f32(O.f64_to_bf16_bits_vec(ref[fin])).astype(np.float64))
+    assert np.array_equal(y[~fin & ~np.isnan(ref)], ref[~fin & ~np.isnan(ref)])
+
+
 def test_tolerance_rejects_planted_mistakes(oracle):
     """A transposed operand, a dropped scale or a wrong group index must fail the bound."""
     rng = np.random.default_rng(9)
