@@ -3,7 +3,7 @@
 // y[M, N] = x[M, K] @ deq(W)[N, K].T, W in nvfp4 (E2M1 nibbles, one E4M3 scale
 // per 16), x bf16, fp32 accumulation, bf16 out.
 //
-// Why bf16 MFMA: an E2M1 value times an E4M3 scale has up to 5 significant bits,
+// Why bf16 MFMA: an E2M1 value times an E4M3 scale has up to 6 significant bits,
 // which no 8-bit MFMA operand format holds, and the scaled MFMAs take only
 // E8M0 scales per 32; in bf16 (8 bits) the dequantized weight is exact.
 //
