@@ -60,6 +60,11 @@ CONFIGS = {
                    workload="nvfp4 lm_head decode GEMV, x bf16 [1,5120], W [248320,5120]"),
     "lmhead_prefill": dict(mode="nvfp4", M=2048, N=248320, K=5120, xscale=1.0,
                            workload="nvfp4 lm_head prefill GEMM, x bf16 [2048,5120], W [248320,5120]"),
+    # short prefill chunks (the last partial chunk, the tokens left after a prefix-cache hit,
+    # src/engine.zig:364-382) on the gate / up projection shape
+    **{f"prefill_m{M}_{mode}": dict(mode=mode, M=M, N=17408, K=5120, xscale=1.0,
+                                    workload=f"{mode} short prefill GEMM, x bf16 [{M},5120], W [17408,5120]")
+       for M in (16, 64, 256) for mode in ("mxfp8", "nvfp4")},
     "mlp_gateup_silu": dict(mode="nvfp4", M=1, N=17408, K=5120, xscale=1.0, mlp=True,
                             workload="nvfp4 MLP gate+up+SiLU*mul fused decode GEMV, x bf16 [1,5120], "
                                      "W_gate, W_up [17408,5120]"),
@@ -119,7 +124,8 @@ def algorithmic(cfg):
 
 
 def roofline_of(cfg, alg, sec_per_call):
-    if cfg["M"] <= 8:
+    peak_mm = MFMA_PEAK_TFLOPS["fp8" if cfg["mode"] == "mxfp8" else "bf16"]
+    if cfg["M"] <= 8 or alg["bytes"] / (HBM_PEAK_GBS * 1e9) >= alg["flops"] / (peak_mm * 1e12):
         achieved = alg["bytes"] / sec_per_call / 1e9
         return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=round(achieved / HBM_PEAK_GBS, 4))

@@ -362,12 +362,17 @@ __device__ __forceinline__ i32x8_t p_frag(const uint8_t *base, int off) {
   return i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
 }
 
-// Tile `bid` of the TS x TS tiling of x rows [0, M) and W rows [n_begin, n_end).
+// Tile `bid` of the TS x TS tiling of x rows [0, M) and W rows [n_begin, n_end), over the
+// K steps [s_begin, s_end).  With `part` null the tile's bf16 result goes to y; otherwise
+// (a K range of a split tile) the fp32 accumulators go to `part` as they sit in the
+// registers: wave w, accumulator (i, j), elements 4 v4 .. 4 v4 + 3 of lane l as the float4
+// at ((w * FI * FJ + i * FJ + j) * 4 + v4) * 64 + l.
 template <int TS>
 __device__ __forceinline__ void pipe_tile(int bid, const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl,
                                           const uint8_t *__restrict__ sh, const uint8_t *__restrict__ sl,
                                           const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
-                                          uint16_t *__restrict__ y, int M, int N, int K, int n_begin, int n_end) {
+                                          uint16_t *__restrict__ y, int M, int N, int K, int n_begin, int n_end,
+                                          int s_begin, int s_end, float *__restrict__ part) {
   using G = PipeGeom<TS>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t lds0 = lds_addr(lds);
@@ -451,9 +456,9 @@ __device__ __forceinline__ void pipe_tile(int bid, const uint8_t *__restrict__ x
   // waits for its DMA(k + 1) (only DMA(k + 2), NDMA loads, may remain), so stage
   // k + 1 is whole before group 0 reads it in interval 2k + 2.
   const int grp = wave >> 2;
-  issue(0);
-  if (steps > 1) issue(1);
-  if (steps > 1) gp_wait_barrier<G::NDMA>();
+  issue(s_begin);
+  if (s_end - s_begin > 1) issue(s_begin + 1);
+  if (s_end - s_begin > 1) gp_wait_barrier<G::NDMA>();
   else gp_wait_barrier<0>();
 
   // one step of a group: loading interval (DMAs of step s + 2 if DMA, fragments of
@@ -500,13 +505,19 @@ __device__ __forceinline__ void pipe_tile(int bid, const uint8_t *__restrict__ x
   auto pp_run = [&](auto grp_c) __attribute__((always_inline)) {
     constexpr int GRP = decltype(grp_c)::value;
     if constexpr (GRP == 1) gp_barrier_only();  // group 1 starts one interval late
-    int s = 0;
-    for (; s + 2 < steps; ++s) pp_step(grp_c, std::true_type{}, s);
-    for (; s < steps; ++s) pp_step(grp_c, std::false_type{}, s);
+    int s = s_begin;
+    for (; s + 2 < s_end; ++s) pp_step(grp_c, std::true_type{}, s);
+    for (; s < s_end; ++s) pp_step(grp_c, std::false_type{}, s);
     if constexpr (GRP == 0) gp_barrier_only();  // matches group 1's extra barrier
   };
   if (grp == 0) pp_run(std::integral_constant<int, 0>{});
   else pp_run(std::integral_constant<int, 1>{});
+
+  if (part) {  // a K range of a split tile: the raw accumulators
+    gp_store_partial<G::FI, G::FJ>(acc, part, wave, lane);
+    return;
+  }
+  (void)steps;
 
   // epilogue through LDS (the ring is idle: every wave has passed the last barrier,
   // after which no fragment read or DMA is outstanding); wave w's region follows w - 1's
@@ -523,24 +534,54 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
     const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
     const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
     uint16_t *__restrict__ y, int M, int N, int K, int n_begin, int n_end) {
-  pipe_tile<TS>(blockIdx.x, xh, xl, sh, sl, w, sw, y, M, N, K, n_begin, n_end);
+  pipe_tile<TS>(blockIdx.x, xh, xl, sh, sl, w, sw, y, M, N, K, n_begin, n_end, 0, K / P_BK, nullptr);
 }
 
 // Both tilings in one launch: blocks [0, tiles1) are the 256-tiles of W rows [0, n_split),
-// the rest the 128-tiles of W rows [n_split, N).  Blocks start in index order as CUs
-// free up, so a CU that finishes its last 256-tile early takes a 128-tile at once
-// instead of waiting for the slowest CU at a kernel boundary.  (The host gives tiles1
-// as whole rounds, a multiple of the CU count, so on a CU count that is a multiple of 8
-// both parts keep their XCD-aware tile order; any tiles1 gives the same results.)
+// the rest cover W rows [n_split, N) one of two ways:
+//   * S == 0: as 128-tiles;
+//   * S >= 2: as 256-tiles whose K steps are split S ways (split tiles): block tiles1 + u
+//     runs K range u % S of tile u / S and leaves its fp32 accumulators in part[u] (256 KiB
+//     each), which gemm_mxfp8_split_reduce_kernel then sums.
+// Blocks start in index order as CUs free up, so a CU that finishes its last 256-tile
+// early takes a tail block at once instead of waiting for the slowest CU at a kernel
+// boundary.  (The host gives tiles1 as whole rounds, a multiple of the CU count, so on a
+// CU count that is a multiple of 8 both parts keep their XCD-aware tile order; any
+// tiles1 gives the same results.)
 __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_split_kernel(
     const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
     const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
-    uint16_t *__restrict__ y, int M, int N, int K, int n_split, int tiles1) {
-  const int b = blockIdx.x;
-  if (b < tiles1)
-    pipe_tile<256>(b, xh, xl, sh, sl, w, sw, y, M, N, K, 0, n_split);
-  else
-    pipe_tile<128>(b - tiles1, xh, xl, sh, sl, w, sw, y, M, N, K, n_split, N);
+    uint16_t *__restrict__ y, int M, int N, int K, int n_split, int tiles1, int S, float *__restrict__ part) {
+  const int b = blockIdx.x, steps = K / P_BK;
+  if (b < tiles1) {
+    pipe_tile<256>(b, xh, xl, sh, sl, w, sw, y, M, N, K, 0, n_split, 0, steps, nullptr);
+  } else if (S == 0) {
+    pipe_tile<128>(b - tiles1, xh, xl, sh, sl, w, sw, y, M, N, K, n_split, N, 0, steps, nullptr);
+  } else {
+    const int u = b - tiles1, t = u / S, k = u - t * S;
+    pipe_tile<256>(t, xh, xl, sh, sl, w, sw, y, M, N, K, n_split, N, k * steps / S, (k + 1) * steps / S,
+                   part + (size_t)u * 256 * 256);
+  }
+}
+
+// The split tiles' results: block b sums wave b % 8's accumulators of split tile b / 8 over
+// its S K ranges, in K order (the same order whichever block finished first, so the
+// result is deterministic), and stores them to y as bf16 like the tile epilogue.
+__global__ __launch_bounds__(64) void gemm_mxfp8_split_reduce_kernel(const float *__restrict__ part,
+                                                                      uint16_t *__restrict__ y, int M, int N,
+                                                                      int n_split, int S) {
+  using G = PipeGeom<256>;
+  constexpr int REGION = 32 * G::FI * (64 * G::FJ + 32);
+  __shared__ __attribute__((aligned(16))) uint8_t region[REGION];
+  const int t = blockIdx.x >> 3, wave = blockIdx.x & 7, lane = threadIdx.x;
+  f32x16_t acc[G::FI][G::FJ];
+  gp_sum_partials<G::FI, G::FJ>(acc, part, t, S, wave, lane);
+  int tm, tn;
+  tile_of(t, (M + 255) / 256, (N - n_split + 255) / 256, &tm, &tn);
+  const int wm = wave >> 1, wn = wave & 1;
+  const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
+  gp_store_tile_bf16<G::FI, G::FJ, 0, G::FI>(acc, region, lane, y, M, N, tm * 256 + wm * 64,
+                                             n_split + tn * 256 + wn * 128, N, vec);
 }
 
 // K % 128: whole step pairs (the tile-major scale layout); W rows must be 16-byte
@@ -572,10 +613,48 @@ bool gemm_mxfp8_ok(const QmmArgs &a) {
 // Workspace: x hi, x lo (M x K bytes each), x hi / lo scales, and for the pipelined
 // kernel the W scales repacked, each scale array padded to whole 256-row tiles.
 
+// How the pipelined GEMM covers the 256-tiles of a call on `cus` CUs:
+//   * a call of at most half as many tiles as CUs (short prefill chunks, narrow
+//     projections) runs every tile split S ways along K (S >= 2, at most one round of
+//     blocks, each at least 8 K steps): n_split = 0, tail_tiles = all tiles;
+//   * otherwise whole rounds of 256-tiles over W rows [0, n_split), and when the last
+//     partial round is whole W tile-columns and four times as many 128-tiles fit one
+//     round, those columns [n_split, N) run as 128-tiles (S = 0);
+//   * else the last round runs as it falls (n_split = N).
+// (Split tiles for a last partial round of a larger call measured slower at M = 4096,
+// N = 17408, K = 5120: the 64 MiB of partial sums cost more than the 128-tiles lose.)
+struct Fp8Plan {
+  int n_split, tiles1, tail_tiles, S;
+};
+static Fp8Plan fp8_plan(const QmmArgs &a, int cus) {
+  const int tiles_m = (a.M + 255) / 256, tiles_n = (a.N + 255) / 256, steps = a.K / P_BK;
+  const int T = tiles_m * tiles_n;
+  Fp8Plan p{a.N, T, 0, 0};
+  if (cus <= 0) return p;
+  if (2 * T <= cus) {
+    int S = cus / T;
+    if (S > 8) S = 8;
+    if (S > steps / 8) S = steps / 8;
+    if (S >= 2) p = Fp8Plan{0, 0, T, S};
+    return p;
+  }
+  const int rem = T % cus;
+  if (rem == 0 || rem % tiles_m != 0 || 4 * rem > cus || T <= cus) return p;
+  p.n_split = (tiles_n - rem / tiles_m) * 256;
+  p.tiles1 = tiles_m * (tiles_n - rem / tiles_m);
+  return p;
+}
+
 size_t gemm_mxfp8_workspace(const QmmArgs &a) {
   const size_t mk = round256(a.M) * a.K, nbk = (size_t)a.K / 32;
-  const bool repack = gemm_mxfp8_pipe_ok(a) && !a.s_tiled;
-  return 2 * mk + 2 * round256(a.M) * nbk + (repack ? round256(a.N) * nbk : 0) + 256;
+  const bool pipe = gemm_mxfp8_pipe_ok(a);
+  const bool repack = pipe && !a.s_tiled;
+  size_t bytes = 2 * mk + 2 * round256(a.M) * nbk + (repack ? round256(a.N) * nbk : 0);
+  if (pipe) {  // the split tiles' fp32 partials, 256 KiB per block, 256-byte aligned
+    const Fp8Plan p = fp8_plan(a, device_cu_count());
+    if (p.S >= 2) bytes = round256(bytes) + (size_t)p.tail_tiles * p.S * 256 * 256 * 4;
+  }
+  return bytes + 256;
 }
 
 size_t tiled_scales_bytes(int64_t N, int nb) { return (size_t)round256((size_t)N) * (size_t)nb; }
@@ -628,26 +707,31 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
     if (e != hipSuccess) return e;
     const int cus = device_cu_count();
     if (cus <= 0) return hipErrorNoDevice;
-    // One block per CU at a time (the ring fills most of a CU's LDS).  When the
-    // 256-tiles leave a last round that a whole number of W tile-columns fills
-    // and four times as many 128-tiles still fit one round, those columns run
-    // as 128-tiles: a quarter of the work per block, all in one round.
-    const int tiles_m = (a.M + 255) / 256, tiles_n = (a.N + 255) / 256;
-    const int rem = (tiles_m * tiles_n) % cus;
-    int n_split = a.N;
-    if (rem != 0 && rem % tiles_m == 0 && 4 * rem <= cus && tiles_m * tiles_n > cus) {
-      const int cols = rem / tiles_m;
-      n_split = (tiles_n - cols) * 256;
-    }
-    const int tiles1 = tiles_m * ((n_split + 255) / 256);
-    if (n_split == a.N) {
-      hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel<256>, dim3(tiles1), dim3(F_THREADS), PipeGeom<256>::LDS, st, xh, xl,
-                         sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, 0, n_split);
+    // One block per CU at a time (the ring fills most of a CU's LDS); see fp8_plan for
+    // how the last partial round runs.
+    const Fp8Plan p = fp8_plan(a, cus);
+    if (p.n_split == a.N) {
+      hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel<256>, dim3(p.tiles1), dim3(F_THREADS), PipeGeom<256>::LDS, st, xh, xl,
+                         sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, 0, a.N);
       return hipGetLastError();
     }
-    const int tiles2 = ((a.M + 127) / 128) * ((a.N - n_split + 127) / 128);
-    hipLaunchKernelGGL(gemm_mxfp8_pipe_split_kernel, dim3(tiles1 + tiles2), dim3(F_THREADS), PipeGeom<256>::LDS, st, xh,
-                       xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, n_split, tiles1);
+    if (p.S == 0) {
+      const int tiles2 = ((a.M + 127) / 128) * ((a.N - p.n_split + 127) / 128);
+      hipLaunchKernelGGL(gemm_mxfp8_pipe_split_kernel, dim3(p.tiles1 + tiles2), dim3(F_THREADS), PipeGeom<256>::LDS,
+                         st, xh, xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, p.n_split, p.tiles1, 0,
+                         (float *)nullptr);
+      return hipGetLastError();
+    }
+    // the partials follow the workspace's x split and (when made here) repacked scales
+    const size_t part_off = round256(2 * mk + 2 * round256(a.M) * nbk + (a.s_tiled ? 0 : round256(a.N) * nbk));
+    float *part = (float *)((uint8_t *)ws + part_off);
+    hipLaunchKernelGGL(gemm_mxfp8_pipe_split_kernel, dim3(p.tiles1 + p.tail_tiles * p.S), dim3(F_THREADS),
+                       PipeGeom<256>::LDS, st, xh, xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, p.n_split,
+                       p.tiles1, p.S, part);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel, dim3(p.tail_tiles * 8), dim3(64), 0, st, (const float *)part,
+                       (uint16_t *)a.y, a.M, a.N, p.n_split, p.S);
     return hipGetLastError();
   }
   static std::atomic<uint64_t> lds_set{0};

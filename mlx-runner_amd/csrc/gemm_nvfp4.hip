@@ -80,11 +80,13 @@ __device__ __forceinline__ bf16x8_t deq8_nvfp4(uint32_t word, uint32_t scale_byt
 }
 
 // Tile `bid` of the TM x 256 tiling of x rows [0, M) and W rows [n_begin, n_end)
-// (n_begin a multiple of 256).
+// (n_begin a multiple of 256), over the K steps [s_begin, s_end).  With `part` null the
+// tile's bf16 result goes to y; otherwise (a K range of a split tile) the fp32
+// accumulators go to `part` (gp_store_partial's layout).
 template <int TM>
 __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x, const uint8_t *__restrict__ w,
                                         const uint8_t *__restrict__ sp, uint16_t *__restrict__ y, int M, int N, int K,
-                                        int n_begin, int n_end) {
+                                        int n_begin, int n_end, int s_begin, int s_end, float *__restrict__ part) {
   using G = NvGeom<TM>;
   constexpr int FI = G::FI, WM = TM / 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -156,9 +158,9 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   // interval); at the barrier ending interval 2k + 1 every wave waits for its
   // DMA(k + 1) (only DMA(k + 2), DMA_S / DMA loads, may remain in flight).
   const int grp = wave >> 2;
-  issue(0);
-  if (steps > 1) issue(1);
-  if (steps <= 1) gp_wait_barrier<0>();
+  issue(s_begin);
+  if (s_end - s_begin > 1) issue(s_begin + 1);
+  if (s_end - s_begin <= 1) gp_wait_barrier<0>();
   else if (sw) gp_wait_barrier<G::DMA_S>();
   else gp_wait_barrier<G::DMA>();
 
@@ -229,13 +231,18 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   auto pp_run = [&](auto grp_c) __attribute__((always_inline)) {
     constexpr int GRP = decltype(grp_c)::value;
     if constexpr (GRP == 1) gp_barrier_only();  // group 1 starts one interval late
-    int s = 0;
-    for (; s + 2 < steps; ++s) pp_step(grp_c, std::true_type{}, s);
-    for (; s < steps; ++s) pp_step(grp_c, std::false_type{}, s);
+    int s = s_begin;
+    for (; s + 2 < s_end; ++s) pp_step(grp_c, std::true_type{}, s);
+    for (; s < s_end; ++s) pp_step(grp_c, std::false_type{}, s);
     if constexpr (GRP == 0) gp_barrier_only();  // matches group 1's extra barrier
   };
   if (grp == 0) pp_run(std::integral_constant<int, 0>{});
   else pp_run(std::integral_constant<int, 1>{});
+  if (part) {  // a K range of a split tile: the raw accumulators
+    gp_store_partial<FI, 2>(acc, part, wave, lane);
+    return;
+  }
+  (void)steps;
 
   // epilogue through LDS (the ring is idle: every wave has passed the last barrier, after
   // which no fragment read or DMA is outstanding), in two halves of the wave's 128 rows
@@ -253,7 +260,39 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
                                                                     const uint8_t *__restrict__ w,
                                                                     const uint8_t *__restrict__ sp,
                                                                     uint16_t *__restrict__ y, int M, int N, int K) {
-  nv_tile<256>(blockIdx.x, x, w, sp, y, M, N, K, 0, N);
+  nv_tile<256>(blockIdx.x, x, w, sp, y, M, N, K, 0, N, 0, K / V_BK, nullptr);
+}
+
+// Every TM x 256 tile split S ways along K: block b runs K range b % S of tile b / S and
+// leaves its fp32 accumulators in slot b of `part` (TM KiB each); gemm_nvfp4_split_reduce
+// then sums them.  For calls of fewer tiles than CUs (short prefill chunks, narrow
+// projections), which would otherwise leave most CUs idle.
+template <int TM>
+__global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_ksplit_kernel(const uint16_t *__restrict__ x,
+                                                                           const uint8_t *__restrict__ w,
+                                                                           const uint8_t *__restrict__ sp,
+                                                                           uint16_t *__restrict__ y, int M, int N,
+                                                                           int K, int S, float *__restrict__ part) {
+  const int b = blockIdx.x, t = b / S, k = b - t * S, steps = K / V_BK;
+  nv_tile<TM>(t, x, w, sp, y, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S, part + (size_t)b * TM * 256);
+}
+
+// The split tiles' results: block b sums wave b % 8's accumulators of tile b / 8 over its S
+// K ranges (in K order) and stores them to y as bf16, as the tile epilogue does.
+template <int TM>
+__global__ __launch_bounds__(64) void gemm_nvfp4_split_reduce_kernel(const float *__restrict__ part,
+                                                                      uint16_t *__restrict__ y, int M, int N, int S) {
+  constexpr int FI = NvGeom<TM>::FI, WM = TM / 2;
+  constexpr int REGION = 32 * FI * (64 * 2 + 32);
+  __shared__ __attribute__((aligned(16))) uint8_t region[REGION];
+  const int t = blockIdx.x >> 3, wave = blockIdx.x & 7, lane = threadIdx.x;
+  f32x16_t acc[FI][2];
+  gp_sum_partials<FI, 2>(acc, part, t, S, wave, lane);
+  int tm, tn;
+  tile_of(t, (M + TM - 1) / TM, (N + V_BN - 1) / V_BN, &tm, &tn);
+  const int wm = wave & 1, wn = wave >> 1;
+  const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
+  gp_store_tile_bf16<FI, 2, 0, FI>(acc, region, lane, y, M, N, tm * TM + wm * WM, tn * V_BN + wn * 64, N, vec);
 }
 
 // Both tile heights in one launch: blocks [0, tiles1) are the 256-row tiles of W rows
@@ -265,11 +304,11 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_split_kernel(const 
                                                                           const uint8_t *__restrict__ sp,
                                                                           uint16_t *__restrict__ y, int M, int N,
                                                                           int K, int n_split, int tiles1) {
-  const int b = blockIdx.x;
+  const int b = blockIdx.x, steps = K / V_BK;
   if (b < tiles1)
-    nv_tile<256>(b, x, w, sp, y, M, N, K, 0, n_split);
+    nv_tile<256>(b, x, w, sp, y, M, N, K, 0, n_split, 0, steps, nullptr);
   else
-    nv_tile<128>(b - tiles1, x, w, sp, y, M, N, K, n_split, N);
+    nv_tile<128>(b - tiles1, x, w, sp, y, M, N, K, n_split, N, 0, steps, nullptr);
 }
 
 static size_t round256v(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -281,8 +320,30 @@ bool gemm_nvfp4_ok(const QmmArgs &a) {
          (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.w % 16 == 0 && (uintptr_t)a.s % 4 == 0;
 }
 
-// Workspace: the scales repacked tile-major, unless they come so (a.s_tiled).
-size_t gemm_nvfp4_workspace(const QmmArgs &a) { return a.s_tiled ? 0 : round256v(a.N) * (size_t)(a.K / 16) + 256; }
+// A call of at most half as many tiles as CUs runs every tile split S ways along K (at
+// most one round of blocks, each at least 8 K steps), with 128-row tiles when x has at
+// most 128 rows: the split plan, or S = 0 for the whole-tile paths.
+struct NvSplit {
+  int TM, tiles, S;
+};
+static NvSplit nv_split_plan(const QmmArgs &a, int cus) {
+  const int TM = a.M <= 128 ? 128 : 256;
+  const int T = ((a.M + TM - 1) / TM) * ((a.N + V_BN - 1) / V_BN), steps = a.K / V_BK;
+  if (cus <= 0 || 2 * T > cus) return NvSplit{TM, T, 0};
+  int S = cus / T;
+  if (S > 8) S = 8;
+  if (S > steps / 8) S = steps / 8;
+  return NvSplit{TM, T, S >= 2 ? S : 0};
+}
+
+// Workspace: the scales repacked tile-major, unless they come so (a.s_tiled), then (split
+// tiles) the fp32 partial sums, TM KiB per block, 256-byte aligned.
+size_t gemm_nvfp4_workspace(const QmmArgs &a) {
+  size_t bytes = a.s_tiled ? 0 : round256v(a.N) * (size_t)(a.K / 16);
+  const NvSplit p = nv_split_plan(a, device_cu_count());
+  if (p.S) bytes = round256v(bytes) + (size_t)p.tiles * p.S * p.TM * 256 * 4;
+  return bytes + 256;
+}
 
 hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
   if (!gemm_nvfp4_ok(a)) return hipErrorInvalidValue;
@@ -293,10 +354,33 @@ hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
     if (e != hipSuccess) return e;
     tiled = (const uint8_t *)ws;
   }
-  static std::atomic<uint64_t> lds_set{0}, lds_split{0};
+  static std::atomic<uint64_t> lds_set{0}, lds_split{0}, lds_k256{0}, lds_k128{0};
   e = ensure_dynamic_lds(lds_set, (const void *)gemm_nvfp4_pipe_kernel, (int)V_LDS);
   if (e == hipSuccess) e = ensure_dynamic_lds(lds_split, (const void *)gemm_nvfp4_pipe_split_kernel, (int)V_LDS);
+  if (e == hipSuccess) e = ensure_dynamic_lds(lds_k256, (const void *)gemm_nvfp4_pipe_ksplit_kernel<256>, (int)V_LDS);
+  if (e == hipSuccess) e = ensure_dynamic_lds(lds_k128, (const void *)gemm_nvfp4_pipe_ksplit_kernel<128>, (int)V_LDS);
   if (e != hipSuccess) return e;
+  const NvSplit sp = nv_split_plan(a, device_cu_count());
+  if (sp.S) {
+    float *part = (float *)((uint8_t *)ws + round256v(a.s_tiled ? 0 : round256v(a.N) * (size_t)(a.K / 16)));
+    const int blocks = sp.tiles * sp.S;
+    if (sp.TM == 128) {
+      hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit_kernel<128>, dim3(blocks), dim3(V_THREADS), V_LDS, st,
+                         (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, sp.S, part);
+      e = hipGetLastError();
+      if (e == hipSuccess)
+        hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<128>, dim3(sp.tiles * 8), dim3(64), 0, st,
+                           (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
+    } else {
+      hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit_kernel<256>, dim3(blocks), dim3(V_THREADS), V_LDS, st,
+                         (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, sp.S, part);
+      e = hipGetLastError();
+      if (e == hipSuccess)
+        hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<256>, dim3(sp.tiles * 8), dim3(64), 0, st,
+                           (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
+    }
+    return e == hipSuccess ? hipGetLastError() : e;
+  }
   // When the 256 x 256 tiles leave a partial last round of whole tile-columns that half
   // the CUs or fewer would run, those columns run as 128 x 256 tiles in the same launch.
   const int tiles_m = (a.M + V_BM - 1) / V_BM, tiles_n = (a.N + V_BN - 1) / V_BN;

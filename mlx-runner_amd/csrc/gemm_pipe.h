@@ -122,6 +122,51 @@ __device__ __forceinline__ void gp_store_tile_bf16(const f32x16_t (&acc)[FI][FJ]
   }
 }
 
+// Split tiles (a tile's K steps run by S blocks): each block stores its wave's FI x FJ
+// fp32 accumulators as they sit in the registers, the float4 of elements 4 v4 .. 4 v4 + 3
+// of accumulator (i, j) of lane l at ((wave * FI * FJ + i * FJ + j) * 4 + v4) * 64 + l of
+// the block's slot (8 waves: 8 * FI * FJ * 1 KiB per slot).
+template <int FI, int FJ>
+__device__ __forceinline__ void gp_store_partial(const f32x16_t (&acc)[FI][FJ], float *__restrict__ slot, int wave,
+                                                 int lane) {
+  float4 *pw = (float4 *)slot + (size_t)wave * FI * FJ * 4 * 64 + lane;
+#pragma unroll
+  for (int i = 0; i < FI; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j)
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4)
+        pw[((i * FJ + j) * 4 + v4) * 64] =
+            make_float4(acc[i][j][4 * v4], acc[i][j][4 * v4 + 1], acc[i][j][4 * v4 + 2], acc[i][j][4 * v4 + 3]);
+}
+
+// One wave's accumulators of split tile t summed over its S slots (t S .. t S + S - 1) in K
+// order, the same order whichever block finished first, so the result is deterministic.
+template <int FI, int FJ>
+__device__ __forceinline__ void gp_sum_partials(f32x16_t (&acc)[FI][FJ], const float *__restrict__ part, int t, int S,
+                                                int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < FI; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  for (int k = 0; k < S; ++k) {
+    const float4 *pw = (const float4 *)part + ((size_t)(t * S + k) * 8 + wave) * FI * FJ * 4 * 64 + lane;
+    float4 f[FI * FJ * 4];
+#pragma unroll
+    for (int q = 0; q < FI * FJ * 4; ++q) f[q] = pw[q * 64];
+#pragma unroll
+    for (int q = 0; q < FI * FJ * 4; ++q) {
+      const int i = q / (FJ * 4), j = (q / 4) % FJ, v4 = q % 4;
+      acc[i][j][4 * v4] += f[q].x;
+      acc[i][j][4 * v4 + 1] += f[q].y;
+      acc[i][j][4 * v4 + 2] += f[q].z;
+      acc[i][j][4 * v4 + 3] += f[q].w;
+    }
+  }
+}
+
 // Weight scales [N, nb bytes] (row-major, as loaded) -> tile-major: for each
 // 256-row tile and each dword column d of the rows, 256 contiguous dwords (one
 // per row): out[((tile * (nb / 4) + d) * 256 + r % 256] = row r's dword d.  A
