@@ -436,7 +436,7 @@ def bench_census(args):
                 wq_, sc_ = mats[i % copies]
                 Q.quantized_matmul(x, wq_, sc_, m, out=y, stream=st)
 
-        for i in range(args.warmup):
+        for i in range(max(args.warmup, copies)):  # every weight copy once (its prefill scale copy)
             step(i, stream)
         torch.cuda.synchronize()
         ms = replay_timed(step, args.steps)
@@ -546,7 +546,10 @@ def measure_qmm(name, args, cache):
         else:
             Q.quantized_matmul(x, wq, sc, mode, out=y, stream=st)
 
-    for i in range(args.warmup):
+    # untimed: at least W steps, and one call on every weight copy (a prefill call's first use
+    # of a scales handle makes its tile-major copy; a graph captured before that would
+    # repack those scales on every replay)
+    for i in range(max(args.warmup, copies)):
         step(i, stream)
     torch.cuda.synchronize()
 

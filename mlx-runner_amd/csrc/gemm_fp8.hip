@@ -514,7 +514,7 @@ __device__ __forceinline__ void pipe_tile(int bid, const uint8_t *__restrict__ x
   else pp_run(std::integral_constant<int, 1>{});
 
   if (part) {  // a K range of a split tile: the raw accumulators
-    gp_store_partial<G::FI, G::FJ>(acc, part, wave, lane);
+    gp_store_partial<G::FI, G::FJ>(acc, part, wave, lane, M - (m0 + wm * (TS / 4)));
     return;
   }
   (void)steps;
@@ -564,24 +564,38 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_split_kernel(
   }
 }
 
-// The split tiles' results: block b sums wave b % 8's accumulators of split tile b / 8 over
-// its S K ranges, in K order (the same order whichever block finished first, so the
-// result is deterministic), and stores them to y as bf16 like the tile epilogue.
+// Every 128-tile split S ways along K, two blocks per CU (the 78 KiB ring and at most 128
+// registers per lane): for x of at most 128 rows, whose 256-tiles would be mostly padding.
+// Block b runs K range b % S of tile b / S into slot b of `part` (64 KiB each).
+__global__ __launch_bounds__(F_THREADS, 2) void gemm_mxfp8_pipe_ksplit128_kernel(
+    const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
+    const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
+    uint16_t *__restrict__ y, int M, int N, int K, int S, float *__restrict__ part) {
+  const int b = blockIdx.x, t = b / S, k = b - t * S, steps = K / P_BK;
+  pipe_tile<128>(t, xh, xl, sh, sl, w, sw, y, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S,
+                 part + (size_t)b * 128 * 128);
+}
+
+// The split tiles' results: block b sums wave b % 8's accumulators of split tile b / 8 (a
+// TS-tile of W rows [n_split, N)) over its S K ranges, in K order (the same order whichever
+// block finished first, so the result is deterministic), and stores them to y as bf16 like
+// the tile epilogue.
+template <int TS>
 __global__ __launch_bounds__(64) void gemm_mxfp8_split_reduce_kernel(const float *__restrict__ part,
                                                                       uint16_t *__restrict__ y, int M, int N,
                                                                       int n_split, int S) {
-  using G = PipeGeom<256>;
+  using G = PipeGeom<TS>;
   constexpr int REGION = 32 * G::FI * (64 * G::FJ + 32);
   __shared__ __attribute__((aligned(16))) uint8_t region[REGION];
   const int t = blockIdx.x >> 3, wave = blockIdx.x & 7, lane = threadIdx.x;
-  f32x16_t acc[G::FI][G::FJ];
-  gp_sum_partials<G::FI, G::FJ>(acc, part, t, S, wave, lane);
   int tm, tn;
-  tile_of(t, (M + 255) / 256, (N - n_split + 255) / 256, &tm, &tn);
+  tile_of(t, (M + TS - 1) / TS, (N - n_split + TS - 1) / TS, &tm, &tn);
   const int wm = wave >> 1, wn = wave & 1;
+  f32x16_t acc[G::FI][G::FJ];
+  gp_sum_partials<G::FI, G::FJ>(acc, part, t, S, wave, lane, M - (tm * TS + wm * (TS / 4)));
   const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
-  gp_store_tile_bf16<G::FI, G::FJ, 0, G::FI>(acc, region, lane, y, M, N, tm * 256 + wm * 64,
-                                             n_split + tn * 256 + wn * 128, N, vec);
+  gp_store_tile_bf16<G::FI, G::FJ, 0, G::FI>(acc, region, lane, y, M, N, tm * TS + wm * (TS / 4),
+                                             n_split + tn * TS + wn * (TS / 2), N, vec);
 }
 
 // K % 128: whole step pairs (the tile-major scale layout); W rows must be 16-byte
@@ -623,19 +637,30 @@ bool gemm_mxfp8_ok(const QmmArgs &a) {
 //   * else the last round runs as it falls (n_split = N).
 // (Split tiles for a last partial round of a larger call measured slower at M = 4096,
 // N = 17408, K = 5120: the 64 MiB of partial sums cost more than the 128-tiles lose.)
+// x of at most 128 rows with at most one 128-tile per CU splits 128-tiles instead, two
+// blocks per CU (TS = 128).
 struct Fp8Plan {
-  int n_split, tiles1, tail_tiles, S;
+  int n_split, tiles1, tail_tiles, S, TS;
 };
+static int fp8_split_ways(int tiles, int capacity, int steps) {
+  int S = capacity / tiles;
+  if (S > 8) S = 8;
+  if (S > steps / 8) S = steps / 8;
+  return S >= 2 ? S : 0;
+}
 static Fp8Plan fp8_plan(const QmmArgs &a, int cus) {
   const int tiles_m = (a.M + 255) / 256, tiles_n = (a.N + 255) / 256, steps = a.K / P_BK;
   const int T = tiles_m * tiles_n;
-  Fp8Plan p{a.N, T, 0, 0};
+  Fp8Plan p{a.N, T, 0, 0, 256};
   if (cus <= 0) return p;
+  const int T128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+  if (a.M <= 128 && T128 <= cus) {
+    const int S = fp8_split_ways(T128, 2 * cus, steps);
+    if (S) return Fp8Plan{0, 0, T128, S, 128};
+  }
   if (2 * T <= cus) {
-    int S = cus / T;
-    if (S > 8) S = 8;
-    if (S > steps / 8) S = steps / 8;
-    if (S >= 2) p = Fp8Plan{0, 0, T, S};
+    const int S = fp8_split_ways(T, cus, steps);
+    if (S) p = Fp8Plan{0, 0, T, S, 256};
     return p;
   }
   const int rem = T % cus;
@@ -652,7 +677,7 @@ size_t gemm_mxfp8_workspace(const QmmArgs &a) {
   size_t bytes = 2 * mk + 2 * round256(a.M) * nbk + (repack ? round256(a.N) * nbk : 0);
   if (pipe) {  // the split tiles' fp32 partials, 256 KiB per block, 256-byte aligned
     const Fp8Plan p = fp8_plan(a, device_cu_count());
-    if (p.S >= 2) bytes = round256(bytes) + (size_t)p.tail_tiles * p.S * 256 * 256 * 4;
+    if (p.S >= 2) bytes = round256(bytes) + (size_t)p.tail_tiles * p.S * p.TS * p.TS * 4;
   }
   return bytes + 256;
 }
@@ -725,13 +750,25 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
     // the partials follow the workspace's x split and (when made here) repacked scales
     const size_t part_off = round256(2 * mk + 2 * round256(a.M) * nbk + (a.s_tiled ? 0 : round256(a.N) * nbk));
     float *part = (float *)((uint8_t *)ws + part_off);
+    if (p.TS == 128) {
+      static std::atomic<uint64_t> lds128{0};
+      e = ensure_dynamic_lds(lds128, (const void *)gemm_mxfp8_pipe_ksplit128_kernel, (int)PipeGeom<128>::LDS);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(gemm_mxfp8_pipe_ksplit128_kernel, dim3(p.tail_tiles * p.S), dim3(F_THREADS),
+                         PipeGeom<128>::LDS, st, xh, xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, p.S, part);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel<128>, dim3(p.tail_tiles * 8), dim3(64), 0, st,
+                         (const float *)part, (uint16_t *)a.y, a.M, a.N, 0, p.S);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL(gemm_mxfp8_pipe_split_kernel, dim3(p.tiles1 + p.tail_tiles * p.S), dim3(F_THREADS),
                        PipeGeom<256>::LDS, st, xh, xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, p.n_split,
                        p.tiles1, p.S, part);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel, dim3(p.tail_tiles * 8), dim3(64), 0, st, (const float *)part,
-                       (uint16_t *)a.y, a.M, a.N, p.n_split, p.S);
+    hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel<256>, dim3(p.tail_tiles * 8), dim3(64), 0, st,
+                       (const float *)part, (uint16_t *)a.y, a.M, a.N, p.n_split, p.S);
     return hipGetLastError();
   }
   static std::atomic<uint64_t> lds_set{0};

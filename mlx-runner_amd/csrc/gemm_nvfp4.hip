@@ -88,12 +88,19 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
                                         const uint8_t *__restrict__ sp, uint16_t *__restrict__ y, int M, int N, int K,
                                         int n_begin, int n_end, int s_begin, int s_end, float *__restrict__ part) {
   using G = NvGeom<TM>;
-  constexpr int FI = G::FI, WM = TM / 2;
+  // Wave layout: 2 (x rows) x 4 (W rows), waves of TM / 2 x 64, or at TM = 64 1 x 8, waves
+  // of 64 x 32, so that each W element is dequantized by one wave of the block (at short x
+  // the dequantization, not the MFMA work, is what a step costs).
+  constexpr bool COLS = TM == 64;
+  constexpr int XD = G::FI;                // x DMAs per wave per step
+  constexpr int FI = COLS ? 2 : TM / 64;   // x fragments (32 rows) per wave
+  constexpr int FJ = COLS ? 1 : 2;         // W fragments (32 rows) per wave
+  constexpr int WM = COLS ? TM : TM / 2, WN = 32 * FJ;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t lds0 = lds_addr(lds);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;  // wave tile: rows wm * WM + [0, WM), cols wn * 64 + [0, 64)
+  const int wm = COLS ? 0 : wave & 1, wn = COLS ? wave : wave >> 1;  // rows wm WM + [0, WM), cols wn WN + [0, WN)
   int tm, tn;
   tile_of(bid, (M + TM - 1) / TM, (n_end - n_begin + V_BN - 1) / V_BN, &tm, &tn);
   const int m0 = tm * TM, n0 = n_begin + tn * V_BN;
@@ -101,9 +108,9 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   const int64_t wrow = K >> 1;  // bytes per W row
 
   // DMA sources (step 0).  x: wave-instruction g = wave + 8 i fills slots q = 64 g + lane.
-  const uint8_t *ga[FI];
+  const uint8_t *ga[XD];
 #pragma unroll
-  for (int i = 0; i < FI; ++i) {
+  for (int i = 0; i < XD; ++i) {
     const int g = wave + 8 * i;
     const int q = 64 * g + lane, row = q >> 3, part = (q & 7) ^ aswz(row);
     ga[i] = (const uint8_t *)x + ((int64_t)min(m0 + row, M - 1) * K + part * 8) * 2;
@@ -118,7 +125,7 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   auto issue = [&](int s) __attribute__((always_inline)) {
     const uint32_t st = lds0 + (uint32_t)((s % V_STAGES) * G::STAGE);
 #pragma unroll
-    for (int i = 0; i < FI; ++i) gp_dma16(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
+    for (int i = 0; i < XD; ++i) gp_dma16(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
     gp_dma16(gw + s * 32, st + G::ATILE + wave * 1024);
     if (sw) gp_dma16(gs + s * 1024, st + G::ATILE + V_WTILE);
   };
@@ -127,7 +134,7 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   // sub-step ks, the step's elements 32 fh + 8 ks + [0, 8) with fh = l / 32:
   // x slot 4 fh + ks, W dword 4 fh + ks)
   const int fr = lane & 31, fh = lane >> 5;
-  int oa[FI], ab[FI], ob[2], os[2];
+  int oa[FI], ab[FI], ob[FJ], os[FJ];
 #pragma unroll
   for (int i = 0; i < FI; ++i) {
     const int r = wm * WM + i * 32 + fr;
@@ -135,17 +142,17 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
     ab[i] = (4 * fh) ^ aswz(r);  // physical slot of logical slot 4 fh + ks is ks ^ ab
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = wn * 64 + j * 32 + fr;
+  for (int j = 0; j < FJ; ++j) {
+    const int r = wn * WN + j * 32 + fr;
     ob[j] = G::ATILE + r * 32 + 16 * (fh ^ wswz(r));
     os[j] = G::ATILE + V_WTILE + r * 4;
   }
 
-  f32x16_t acc[FI][2];
+  f32x16_t acc[FI][FJ];
 #pragma unroll
   for (int i = 0; i < FI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < FJ; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
@@ -169,20 +176,20 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
     constexpr bool DMA = decltype(dma_c)::value;
     if constexpr (DMA && GRP == 1) issue(s + 2);  // interval 2s + 1
     const uint8_t *st = lds + (s % V_STAGES) * G::STAGE;
-    uint4 wq[2];
-    uint32_t wsc[2];
+    uint4 wq[FJ];
+    uint32_t wsc[FJ];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < FJ; ++j) {
       wq[j] = *(const uint4 *)(st + ob[j]);
       wsc[j] = *(const uint32_t *)(st + os[j]);
     }
     // W is dequantized here, in the loading interval, so that this VALU work runs
     // beside the other group's MFMAs and the computing interval is MFMAs only
-    bf16x8_t bf[4][2];
+    bf16x8_t bf[4][FJ];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < FJ; ++j) {
         const uint32_t word = ks == 0 ? wq[j].x : ks == 1 ? wq[j].y : ks == 2 ? wq[j].z : wq[j].w;
         bf[ks][j] = deq8_nvfp4(word, (wsc[j] >> (8 * (2 * fh + (ks >> 1)))) & 0xFF);  // group 2 fh + ks / 2
       }
@@ -206,7 +213,7 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
           af[(ks + 1) & 1][i] = *(const bf16x8_t *)(st + oa[i] + 16 * ((ks + 1) ^ ab[i]));
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < FJ; ++j)
 #pragma unroll
         for (int i = 0; i < FI; ++i)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bf[ks][j], acc[i][j], 0, 0, 0);
@@ -214,10 +221,10 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
     // keep that order: the scheduler would otherwise sink each read next to its use
 #pragma unroll
     for (int ks = 0; ks < 3; ++ks) {
-      __builtin_amdgcn_sched_group_barrier(0x100, FI, 0);      // FI LDS reads (sub-step ks + 1)
-      __builtin_amdgcn_sched_group_barrier(0x008, 2 * FI, 0);  // then sub-step ks's MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, FI, 0);       // FI LDS reads (sub-step ks + 1)
+      __builtin_amdgcn_sched_group_barrier(0x008, FJ * FI, 0);  // then sub-step ks's MFMAs
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2 * FI, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, FJ * FI, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (GRP == 1) gp_lds_barrier();
     else if constexpr (DMA) {
@@ -239,7 +246,7 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   if (grp == 0) pp_run(std::integral_constant<int, 0>{});
   else pp_run(std::integral_constant<int, 1>{});
   if (part) {  // a K range of a split tile: the raw accumulators
-    gp_store_partial<FI, 2>(acc, part, wave, lane);
+    gp_store_partial<FI, FJ>(acc, part, wave, lane, M - (m0 + wm * WM));
     return;
   }
   (void)steps;
@@ -247,13 +254,15 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   // epilogue through LDS (the ring is idle: every wave has passed the last barrier, after
   // which no fragment read or DMA is outstanding), in two halves of the wave's 128 rows
   // so that the eight regions fit the ring
-  constexpr int REGION = 64 * (64 * 2 + 32);
-  static_assert(8 * REGION <= V_LDS, "the epilogue regions fit the launch's ring");
+  constexpr int NI = FI < 2 ? FI : 2;  // accumulator rows per half
+  constexpr int REGION = 32 * NI * (64 * FJ + 32);
+  // (the 256- and 128-row instances run with the 256-row ring, the 64-row one with its own)
+  static_assert(8 * REGION <= (TM == 64 ? G::LDS : V_LDS), "the epilogue regions fit the launch's ring");
   const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
   uint8_t *region = lds + wave * REGION;
-  gp_store_tile_bf16<FI, 2, 0, 2>(acc, region, lane, y, M, N, m0 + wm * WM, n0 + wn * 64, n_end, vec);
+  gp_store_tile_bf16<FI, FJ, 0, NI>(acc, region, lane, y, M, N, m0 + wm * WM, n0 + wn * WN, n_end, vec);
   if constexpr (FI == 4)
-    gp_store_tile_bf16<FI, 2, 2, 2>(acc, region, lane, y, M, N, m0 + wm * WM, n0 + wn * 64, n_end, vec);
+    gp_store_tile_bf16<FI, FJ, 2, 2>(acc, region, lane, y, M, N, m0 + wm * WM, n0 + wn * WN, n_end, vec);
 }
 
 __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16_t *__restrict__ x,
@@ -266,15 +275,31 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
 // Every TM x 256 tile split S ways along K: block b runs K range b % S of tile b / S and
 // leaves its fp32 accumulators in slot b of `part` (TM KiB each); gemm_nvfp4_split_reduce
 // then sums them.  For calls of fewer tiles than CUs (short prefill chunks, narrow
-// projections), which would otherwise leave most CUs idle.
+// projections), which would otherwise leave most CUs idle.  The 64-row instance (x of at
+// most 64 rows) moves 17 KiB per K step and runs two blocks per CU (its 51 KiB ring and
+// at most 128 registers per lane), so a CU keeps two blocks' loads in flight.
+template <int TM>
+__device__ __forceinline__ void nv_ksplit_block(const uint16_t *__restrict__ x, const uint8_t *__restrict__ w,
+                                                const uint8_t *__restrict__ sp, uint16_t *__restrict__ y, int M,
+                                                int N, int K, int S, float *__restrict__ part) {
+  const int b = blockIdx.x, t = b / S, k = b - t * S, steps = K / V_BK;
+  nv_tile<TM>(t, x, w, sp, y, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S, part + (size_t)b * TM * 256);
+}
 template <int TM>
 __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_ksplit_kernel(const uint16_t *__restrict__ x,
                                                                            const uint8_t *__restrict__ w,
                                                                            const uint8_t *__restrict__ sp,
                                                                            uint16_t *__restrict__ y, int M, int N,
                                                                            int K, int S, float *__restrict__ part) {
-  const int b = blockIdx.x, t = b / S, k = b - t * S, steps = K / V_BK;
-  nv_tile<TM>(t, x, w, sp, y, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S, part + (size_t)b * TM * 256);
+  nv_ksplit_block<TM>(x, w, sp, y, M, N, K, S, part);
+}
+__global__ __launch_bounds__(V_THREADS, 2) void gemm_nvfp4_pipe_ksplit64_kernel(const uint16_t *__restrict__ x,
+                                                                                const uint8_t *__restrict__ w,
+                                                                                const uint8_t *__restrict__ sp,
+                                                                                uint16_t *__restrict__ y, int M,
+                                                                                int N, int K, int S,
+                                                                                float *__restrict__ part) {
+  nv_ksplit_block<64>(x, w, sp, y, M, N, K, S, part);
 }
 
 // The split tiles' results: block b sums wave b % 8's accumulators of tile b / 8 over its S
@@ -282,17 +307,20 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_ksplit_kernel(const
 template <int TM>
 __global__ __launch_bounds__(64) void gemm_nvfp4_split_reduce_kernel(const float *__restrict__ part,
                                                                       uint16_t *__restrict__ y, int M, int N, int S) {
-  constexpr int FI = NvGeom<TM>::FI, WM = TM / 2;
-  constexpr int REGION = 32 * FI * (64 * 2 + 32);
+  // the wave layout of nv_tile<TM>
+  constexpr bool COLS = TM == 64;
+  constexpr int FI = COLS ? 2 : TM / 64, FJ = COLS ? 1 : 2;
+  constexpr int WM = COLS ? TM : TM / 2, WN = 32 * FJ;
+  constexpr int REGION = 32 * FI * (64 * FJ + 32);
   __shared__ __attribute__((aligned(16))) uint8_t region[REGION];
   const int t = blockIdx.x >> 3, wave = blockIdx.x & 7, lane = threadIdx.x;
-  f32x16_t acc[FI][2];
-  gp_sum_partials<FI, 2>(acc, part, t, S, wave, lane);
   int tm, tn;
   tile_of(t, (M + TM - 1) / TM, (N + V_BN - 1) / V_BN, &tm, &tn);
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = COLS ? 0 : wave & 1, wn = COLS ? wave : wave >> 1;
+  f32x16_t acc[FI][FJ];
+  gp_sum_partials<FI, FJ>(acc, part, t, S, wave, lane, M - (tm * TM + wm * WM));
   const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
-  gp_store_tile_bf16<FI, 2, 0, FI>(acc, region, lane, y, M, N, tm * TM + wm * WM, tn * V_BN + wn * 64, N, vec);
+  gp_store_tile_bf16<FI, FJ, 0, FI>(acc, region, lane, y, M, N, tm * TM + wm * WM, tn * V_BN + wn * WN, N, vec);
 }
 
 // Both tile heights in one launch: blocks [0, tiles1) are the 256-row tiles of W rows
@@ -321,16 +349,17 @@ bool gemm_nvfp4_ok(const QmmArgs &a) {
 }
 
 // A call of at most half as many tiles as CUs runs every tile split S ways along K (at
-// most one round of blocks, each at least 8 K steps), with 128-row tiles when x has at
-// most 128 rows: the split plan, or S = 0 for the whole-tile paths.
+// most one round of blocks, each at least 8 K steps), with 64-row tiles (two blocks per
+// CU) when x has at most 64 rows and 128-row tiles up to 128 rows: the split plan, or
+// S = 0 for the whole-tile paths.
 struct NvSplit {
   int TM, tiles, S;
 };
 static NvSplit nv_split_plan(const QmmArgs &a, int cus) {
-  const int TM = a.M <= 128 ? 128 : 256;
+  const int TM = a.M <= 64 ? 64 : a.M <= 128 ? 128 : 256;
   const int T = ((a.M + TM - 1) / TM) * ((a.N + V_BN - 1) / V_BN), steps = a.K / V_BK;
   if (cus <= 0 || 2 * T > cus) return NvSplit{TM, T, 0};
-  int S = cus / T;
+  int S = (TM == 64 ? 2 * cus : cus) / T;
   if (S > 8) S = 8;
   if (S > steps / 8) S = steps / 8;
   return NvSplit{TM, T, S >= 2 ? S : 0};
@@ -354,17 +383,26 @@ hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
     if (e != hipSuccess) return e;
     tiled = (const uint8_t *)ws;
   }
-  static std::atomic<uint64_t> lds_set{0}, lds_split{0}, lds_k256{0}, lds_k128{0};
+  static std::atomic<uint64_t> lds_set{0}, lds_split{0}, lds_k256{0}, lds_k128{0}, lds_k64{0};
   e = ensure_dynamic_lds(lds_set, (const void *)gemm_nvfp4_pipe_kernel, (int)V_LDS);
   if (e == hipSuccess) e = ensure_dynamic_lds(lds_split, (const void *)gemm_nvfp4_pipe_split_kernel, (int)V_LDS);
   if (e == hipSuccess) e = ensure_dynamic_lds(lds_k256, (const void *)gemm_nvfp4_pipe_ksplit_kernel<256>, (int)V_LDS);
   if (e == hipSuccess) e = ensure_dynamic_lds(lds_k128, (const void *)gemm_nvfp4_pipe_ksplit_kernel<128>, (int)V_LDS);
+  if (e == hipSuccess)
+    e = ensure_dynamic_lds(lds_k64, (const void *)gemm_nvfp4_pipe_ksplit64_kernel, (int)NvGeom<64>::LDS);
   if (e != hipSuccess) return e;
   const NvSplit sp = nv_split_plan(a, device_cu_count());
   if (sp.S) {
     float *part = (float *)((uint8_t *)ws + round256v(a.s_tiled ? 0 : round256v(a.N) * (size_t)(a.K / 16)));
     const int blocks = sp.tiles * sp.S;
-    if (sp.TM == 128) {
+    if (sp.TM == 64) {
+      hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit64_kernel, dim3(blocks), dim3(V_THREADS), NvGeom<64>::LDS, st,
+                         (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, sp.S, part);
+      e = hipGetLastError();
+      if (e == hipSuccess)
+        hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<64>, dim3(sp.tiles * 8), dim3(64), 0, st,
+                           (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
+    } else if (sp.TM == 128) {
       hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit_kernel<128>, dim3(blocks), dim3(V_THREADS), V_LDS, st,
                          (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, sp.S, part);
       e = hipGetLastError();

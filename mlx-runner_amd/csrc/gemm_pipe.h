@@ -125,26 +125,30 @@ __device__ __forceinline__ void gp_store_tile_bf16(const f32x16_t (&acc)[FI][FJ]
 // Split tiles (a tile's K steps run by S blocks): each block stores its wave's FI x FJ
 // fp32 accumulators as they sit in the registers, the float4 of elements 4 v4 .. 4 v4 + 3
 // of accumulator (i, j) of lane l at ((wave * FI * FJ + i * FJ + j) * 4 + v4) * 64 + l of
-// the block's slot (8 waves: 8 * FI * FJ * 1 KiB per slot).
+// the block's slot (8 waves: 8 * FI * FJ * 1 KiB per slot).  Accumulator rows i with
+// 32 i >= live_rows (the wave's rows past the last x row: padding of a short x) are
+// neither stored nor summed.
 template <int FI, int FJ>
 __device__ __forceinline__ void gp_store_partial(const f32x16_t (&acc)[FI][FJ], float *__restrict__ slot, int wave,
-                                                 int lane) {
+                                                 int lane, int live_rows) {
   float4 *pw = (float4 *)slot + (size_t)wave * FI * FJ * 4 * 64 + lane;
 #pragma unroll
-  for (int i = 0; i < FI; ++i)
+  for (int i = 0; i < FI; ++i) {
+    if (32 * i >= live_rows) break;
 #pragma unroll
     for (int j = 0; j < FJ; ++j)
 #pragma unroll
       for (int v4 = 0; v4 < 4; ++v4)
         pw[((i * FJ + j) * 4 + v4) * 64] =
             make_float4(acc[i][j][4 * v4], acc[i][j][4 * v4 + 1], acc[i][j][4 * v4 + 2], acc[i][j][4 * v4 + 3]);
+  }
 }
 
 // One wave's accumulators of split tile t summed over its S slots (t S .. t S + S - 1) in K
 // order, the same order whichever block finished first, so the result is deterministic.
 template <int FI, int FJ>
 __device__ __forceinline__ void gp_sum_partials(f32x16_t (&acc)[FI][FJ], const float *__restrict__ part, int t, int S,
-                                                int wave, int lane) {
+                                                int wave, int lane, int live_rows) {
 #pragma unroll
   for (int i = 0; i < FI; ++i)
 #pragma unroll
@@ -155,7 +159,8 @@ __device__ __forceinline__ void gp_sum_partials(f32x16_t (&acc)[FI][FJ], const f
     const float4 *pw = (const float4 *)part + ((size_t)(t * S + k) * 8 + wave) * FI * FJ * 4 * 64 + lane;
     float4 f[FI * FJ * 4];
 #pragma unroll
-    for (int q = 0; q < FI * FJ * 4; ++q) f[q] = pw[q * 64];
+    for (int q = 0; q < FI * FJ * 4; ++q)
+      f[q] = 32 * (q / (FJ * 4)) < live_rows ? pw[q * 64] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int q = 0; q < FI * FJ * 4; ++q) {
       const int i = q / (FJ * 4), j = (q / 4) % FJ, v4 = q % 4;
