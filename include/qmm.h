@@ -202,7 +202,9 @@ const char *qmm_peek_error_name(void);
 int qmm_take_error(char *buf, size_t len);
 /* Checkpoints: 0 = no error, QMM_ERR_OOM, QMM_ERR_FAILURE; consume the latch.
  * An error the HIP runtime holds for the calling thread (hipGetLastError) is
- * latched first.  They do not wait for the device: an error of work still in
+ * latched first, except hipErrorNotReady (a query's answer) and hipErrorNoDevice.
+ * Every op that launches work clears such a leftover runtime error when it starts,
+ * so an op reports only its own failures, not one the caller's code left behind.  They do not wait for the device: an error of work still in
  * flight surfaces at the call that waits for it (qmm_synchronize,
  * qmm_array_to_host), which latches it, so call qmm_synchronize before a
  * checkpoint that must cover all enqueued work.

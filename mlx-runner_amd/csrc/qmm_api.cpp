@@ -100,6 +100,13 @@ int fail_hip(hipError_t e, const char *what) {
   return fail("[%s] %s: %s", what, hipGetErrorName(e), hipGetErrorString(e));
 }
 
+// Called at the start of every op that launches work: an error the HIP runtime still
+// holds for this thread at that point comes from outside the op (a failed call in the
+// caller's own code, a query's hipErrorNotReady).  The launch helpers read the runtime's
+// last error after each launch, so such a leftover would make the op report a failure
+// it did not have; clearing it first leaves each op reporting only its own.
+void begin_op() { (void)hipGetLastError(); }
+
 // The chokepoint every op returns through: counts ops and applies the armed test fault.
 int finish(int rc) {
   g_op_count.fetch_add(1, std::memory_order_relaxed);
@@ -616,6 +623,7 @@ static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op, vo
 int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array scales, qmm_array biases,
                          bool transpose_w, qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
                          qmm_stream s) {
+  begin_op();
   const char *op = "quantized_matmul";
   if (!res) return finish(fail("[%s] null result pointer", op));
   int m;
@@ -668,6 +676,7 @@ uint64_t qmm_scale_copy_bytes(void) { return g_tiled_bytes.load(std::memory_orde
 int qmm_quantized_matmul_group(qmm_array *res, size_t n, qmm_array x, const qmm_array *w, const qmm_array *scales,
                                qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
                                qmm_stream s) {
+  begin_op();
   const char *op = "quantized_matmul_group";
   if (!res || !w || !scales) return finish(fail("[%s] null argument", op));
   if (n < 1 || n > 4) return finish(fail("[%s] takes 1 to 4 matrices, got %zu", op, n));
@@ -755,6 +764,7 @@ int qmm_quantized_matmul_group(qmm_array *res, size_t n, qmm_array x, const qmm_
 }
 
 int qmm_silu_mul(qmm_array *res, qmm_array g, qmm_array u, qmm_stream s) {
+  begin_op();
   const char *op = "silu_mul";
   if (!res) return finish(fail("[%s] null result pointer", op));
   Arr *ga = (Arr *)g.ctx, *ua = (Arr *)u.ctx;
@@ -824,6 +834,7 @@ static hipError_t gdn_no_steps(const GdnArgs &a, hipStream_t st) {
 
 int qmm_gdn_recurrence(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_array k, qmm_array v, qmm_array g,
                        qmm_array beta, qmm_array state, qmm_dtype y_dtype, qmm_stream s) {
+  begin_op();
   const char *op = "gdn_recurrence";
   if (!y || !state_out) return finish(fail("[%s] null result pointer", op));
   GdnArgs a;
@@ -866,6 +877,7 @@ static int preallocated(const char *op, const char *what, qmm_array *res, const 
 
 int qmm_gdn_recurrence_noalloc(qmm_array *y, qmm_array *state_out, qmm_array q, qmm_array k, qmm_array v,
                                qmm_array g, qmm_array beta, qmm_array state, qmm_dtype y_dtype, qmm_stream s) {
+  begin_op();
   const char *op = "gdn_recurrence_noalloc";
   if (!y || !state_out) return finish(fail("[%s] null result pointer", op));
   GdnArgs a;
@@ -899,6 +911,7 @@ int qmm_gdn_recurrence_noalloc(qmm_array *y, qmm_array *state_out, qmm_array q, 
 int qmm_mlp_gate_up_silu(qmm_array *res, qmm_array x, qmm_array w_gate, qmm_array s_gate, qmm_array w_up,
                          qmm_array s_up, qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
                          qmm_stream s) {
+  begin_op();
   const char *op = "mlp_gate_up_silu";
   if (!res) return finish(fail("[%s] null result pointer", op));
   int m;
@@ -980,6 +993,7 @@ int qmm_mlp_gate_up_silu(qmm_array *res, qmm_array x, qmm_array w_gate, qmm_arra
 int qmm_dequantize(qmm_array *res, qmm_array w, qmm_array scales, qmm_array biases, qmm_optional_int group_size,
                    qmm_optional_int bits, const char *mode, qmm_array global_scale, qmm_optional_dtype dtype,
                    qmm_stream s) {
+  begin_op();
   const char *op = "dequantize";
   if (!res) return finish(fail("[%s] null result pointer", op));
   int m;
@@ -1002,6 +1016,7 @@ int qmm_dequantize(qmm_array *res, qmm_array w, qmm_array scales, qmm_array bias
 
 int qmm_quantize(qmm_vector_array *res, qmm_array w, qmm_optional_int group_size, qmm_optional_int bits,
                  const char *mode, qmm_array global_scale, qmm_stream s) {
+  begin_op();
   const char *op = "quantize";
   if (!res) return finish(fail("[%s] null result pointer", op));
   int m;
@@ -1038,6 +1053,7 @@ int qmm_quantize(qmm_vector_array *res, qmm_array w, qmm_optional_int group_size
 }
 
 int qmm_linear(qmm_array *res, qmm_array x, qmm_array w, qmm_stream s) {
+  begin_op();
   const char *op = "linear";
   if (!res) return finish(fail("[%s] null result pointer", op));
   Arr *xa = (Arr *)x.ctx, *wa = (Arr *)w.ctx;

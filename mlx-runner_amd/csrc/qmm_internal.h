@@ -42,6 +42,9 @@ void latch_error(const char *msg);
 int fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 int fail_hip(hipError_t e, const char *what);
 int finish(int rc);
+// Clears an error the HIP runtime holds for this thread from outside the library (at the
+// start of every op that launches work).
+void begin_op();
 int alloc_device(void **p, size_t bytes, hipStream_t st);
 // Scratch for work enqueued on `st` (at least `bytes`): the stream's grow-only
 // workspace, or while the stream is being captured and that is too small, a

@@ -40,3 +40,31 @@ def test_failed_allocation_reports_out_of_memory():
     finally:
         Q.lib.qmm_array_free(w)
         Q.lib.qmm_array_free(s)
+
+
+@pytest.mark.parametrize("mode,M", [("nvfp4", 1), ("mxfp8", 3), ("nvfp4", 40), ("mxfp8", 300)])
+def test_error_left_by_other_code_is_not_an_op_failure(mode, M):
+    """A HIP error the caller's own code left in the runtime (here hipSetDevice on a device
+    that does not exist, its return code ignored) is not an error of the next op: the op
+    succeeds, its result is right and nothing is latched."""
+    import ctypes
+
+    import numpy as np
+
+    import oracle as O
+
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch and the library share
+    K, N = 1024, 512
+    rng = np.random.default_rng(61 + M)
+    wq, s = O.quantize(mode, O.bf16_bits_to_f32(O.f32_to_bf16_bits(rng.standard_normal((N, K)) * 0.02)))
+    xb = O.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    x, w, sc = Q.Array.from_numpy(xb, Q.BFLOAT16), Q.Array.from_numpy(wq, Q.UINT32), Q.Array.from_numpy(s, Q.UINT8)
+    torch.cuda.synchronize()
+    Q.lib.qmm_reset_faults_for_test()
+    assert hip.hipSetDevice(ctypes.c_int(4096)) != 0  # leaves hipErrorInvalidDevice for this thread
+    y = Q.quantized_matmul(x, w, sc, mode).numpy()
+    assert Q.take_error() is None
+    assert Q.lib.qmm_check_error() == 0
+    ok, fro, worst = O.check_tolerance(O.bf16_bits_to_f32(y), O.bf16_bits_to_f32(O.qmm(mode, xb, wq, s)),
+                                       rel_fro=1e-3, ulps=4.0)
+    assert ok, (fro, worst)
