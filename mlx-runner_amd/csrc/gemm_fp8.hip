@@ -386,8 +386,12 @@ __device__ __forceinline__ void pipe_tile(int bid, const uint8_t *__restrict__ x
 
   // tile DMA: wave-instruction t (< TI) of this wave fills LDS slots q = (8 t + wave) * 64 + lane
   // (x hi / lo pre-tiled: a 256-row block's step is 1024 contiguous slots, rows m0 % 256 on;
-  // W row-major: slot q holds row q >> 2, 16-byte part (q & 3) ^ swz(row))
+  // W row-major: slot q holds row q >> 2, 16-byte part (q & 3) ^ swz(row)).  An x instruction
+  // covers tile rows 16 (8 t + wave) + [0, 16); when all 16 are past the last x row (a short
+  // x) it moves 4 bytes per lane instead of 16: the same instruction count (the waits count
+  // them), a quarter of the bytes, and those rows' results are not stored.
   const uint8_t *ga_h[G::TI], *ga_l[G::TI], *gb[G::TI];
+  bool xdead[G::TI];
 #pragma unroll
   for (int t = 0; t < G::TI; ++t) {
     const int q = (8 * t + wave) * 64 + lane, row = q >> 2, part = (q & 3) ^ p_swz(row);
@@ -395,6 +399,7 @@ __device__ __forceinline__ void pipe_tile(int bid, const uint8_t *__restrict__ x
     ga_h[t] = xh + xo;
     ga_l[t] = xl + xo;
     gb[t] = w + (int64_t)min(n0 + row, N - 1) * K + part * 16;
+    xdead[t] = m0 + 16 * (8 * t + wave) >= M;
   }
   // scale DMA: wave-instruction t = TI wave + h (h < TI) copies rows (t % IPT) * 64 + lane
   // of tensor t / IPT (x hi, x lo, W, all tile-major; the 4th re-reads x hi into the spare block)
@@ -413,8 +418,13 @@ __device__ __forceinline__ void pipe_tile(int bid, const uint8_t *__restrict__ x
     const int64_t xs = (int64_t)s * 16384;
 #pragma unroll
     for (int t = 0; t < G::TI; ++t) {
-      gp_dma16(ga_h[t] + xs, st + (8 * t + wave) * 1024);
-      gp_dma16(ga_l[t] + xs, st + G::TILE + (8 * t + wave) * 1024);
+      if (xdead[t]) {
+        gp_dma4(ga_h[t] + xs, st + (8 * t + wave) * 1024);
+        gp_dma4(ga_l[t] + xs, st + G::TILE + (8 * t + wave) * 1024);
+      } else {
+        gp_dma16(ga_h[t] + xs, st + (8 * t + wave) * 1024);
+        gp_dma16(ga_l[t] + xs, st + G::TILE + (8 * t + wave) * 1024);
+      }
       gp_dma16(gb[t] + k0, st + 2 * G::TILE + (8 * t + wave) * 1024);
     }
     const int so = 1024 * (s >> 1);  // the step pair's block
@@ -576,26 +586,27 @@ __global__ __launch_bounds__(F_THREADS, 2) void gemm_mxfp8_pipe_ksplit128_kernel
                  part + (size_t)b * 128 * 128);
 }
 
-// The split tiles' results: block b sums wave b % 8's accumulators of split tile b / 8 (a
-// TS-tile of W rows [n_split, N)) over its S K ranges, in K order (the same order whichever
-// block finished first, so the result is deterministic), and stores them to y as bf16 like
-// the tile epilogue.
+// The split tiles' results (TS-tiles of W rows [n_split, N)): one thread per float4 of a
+// tile's partial layout (gp_reduce_quad), fp8_reduce_blocks<TS> blocks of 256 per tile.
 template <int TS>
-__global__ __launch_bounds__(64) void gemm_mxfp8_split_reduce_kernel(const float *__restrict__ part,
-                                                                      uint16_t *__restrict__ y, int M, int N,
-                                                                      int n_split, int S) {
+constexpr int fp8_reduce_blocks() {
+  return 2 * PipeGeom<TS>::FI * PipeGeom<TS>::FJ * 4;
+}
+template <int TS>
+__global__ __launch_bounds__(256) void gemm_mxfp8_split_reduce_kernel(const float *__restrict__ part,
+                                                                       uint16_t *__restrict__ y, int M, int N,
+                                                                       int n_split, int S) {
   using G = PipeGeom<TS>;
-  constexpr int REGION = 32 * G::FI * (64 * G::FJ + 32);
-  __shared__ __attribute__((aligned(16))) uint8_t region[REGION];
-  const int t = blockIdx.x >> 3, wave = blockIdx.x & 7, lane = threadIdx.x;
+  constexpr int NQ = G::FI * G::FJ * 4;  // float4s per lane per wave
+  static_assert(8 * NQ * 64 == 256 * fp8_reduce_blocks<TS>(), "whole blocks per tile");
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  const int t = g / (8 * NQ * 64), rem = g - t * (8 * NQ * 64);
+  const int wave = rem / (NQ * 64), q = (rem >> 6) % NQ, lane = rem & 63;
   int tm, tn;
   tile_of(t, (M + TS - 1) / TS, (N - n_split + TS - 1) / TS, &tm, &tn);
   const int wm = wave >> 1, wn = wave & 1;
-  f32x16_t acc[G::FI][G::FJ];
-  gp_sum_partials<G::FI, G::FJ>(acc, part, t, S, wave, lane, M - (tm * TS + wm * (TS / 4)));
-  const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
-  gp_store_tile_bf16<G::FI, G::FJ, 0, G::FI>(acc, region, lane, y, M, N, tm * TS + wm * (TS / 4),
-                                             n_split + tn * TS + wn * (TS / 2), N, vec);
+  gp_reduce_quad<G::FI, G::FJ>(part, y, M, N, N, t, S, wave, q, lane, tm * TS + wm * (TS / 4),
+                               n_split + tn * TS + wn * (TS / 2));
 }
 
 // K % 128: whole step pairs (the tile-major scale layout); W rows must be 16-byte
@@ -758,8 +769,8 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
                          PipeGeom<128>::LDS, st, xh, xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, p.S, part);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel<128>, dim3(p.tail_tiles * 8), dim3(64), 0, st,
-                         (const float *)part, (uint16_t *)a.y, a.M, a.N, 0, p.S);
+      hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel<128>, dim3(p.tail_tiles * fp8_reduce_blocks<128>()), dim3(256), 0,
+                         st, (const float *)part, (uint16_t *)a.y, a.M, a.N, 0, p.S);
       return hipGetLastError();
     }
     hipLaunchKernelGGL(gemm_mxfp8_pipe_split_kernel, dim3(p.tiles1 + p.tail_tiles * p.S), dim3(F_THREADS),
@@ -767,8 +778,8 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
                        p.tiles1, p.S, part);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel<256>, dim3(p.tail_tiles * 8), dim3(64), 0, st,
-                       (const float *)part, (uint16_t *)a.y, a.M, a.N, p.n_split, p.S);
+    hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel<256>, dim3(p.tail_tiles * fp8_reduce_blocks<256>()), dim3(256), 0,
+                       st, (const float *)part, (uint16_t *)a.y, a.M, a.N, p.n_split, p.S);
     return hipGetLastError();
   }
   static std::atomic<uint64_t> lds_set{0};

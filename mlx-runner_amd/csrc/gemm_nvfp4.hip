@@ -107,13 +107,18 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   const int steps = K / V_BK;
   const int64_t wrow = K >> 1;  // bytes per W row
 
-  // DMA sources (step 0).  x: wave-instruction g = wave + 8 i fills slots q = 64 g + lane.
+  // DMA sources (step 0).  x: wave-instruction g = wave + 8 i fills slots q = 64 g + lane,
+  // rows 8 g + [0, 8) of the tile.  When all 8 are past the last x row (a short x), it moves
+  // 4 bytes per lane instead of 16: the same instruction count (the waits count them), a
+  // quarter of the bytes, and those rows' results are not stored.
   const uint8_t *ga[XD];
+  bool xdead[XD];
 #pragma unroll
   for (int i = 0; i < XD; ++i) {
     const int g = wave + 8 * i;
     const int q = 64 * g + lane, row = q >> 3, part = (q & 7) ^ aswz(row);
     ga[i] = (const uint8_t *)x + ((int64_t)min(m0 + row, M - 1) * K + part * 8) * 2;
+    xdead[i] = m0 + 8 * g >= M;
   }
   // W: wave w moves rows 32 w + lane / 2, LDS half lane % 2 of the row (the row's half
   // (lane % 2) ^ wswz(row) of the step's 32 bytes)
@@ -125,7 +130,10 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   auto issue = [&](int s) __attribute__((always_inline)) {
     const uint32_t st = lds0 + (uint32_t)((s % V_STAGES) * G::STAGE);
 #pragma unroll
-    for (int i = 0; i < XD; ++i) gp_dma16(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
+    for (int i = 0; i < XD; ++i) {
+      if (xdead[i]) gp_dma4(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
+      else gp_dma16(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
+    }
     gp_dma16(gw + s * 32, st + G::ATILE + wave * 1024);
     if (sw) gp_dma16(gs + s * 1024, st + G::ATILE + V_WTILE);
   };
@@ -302,25 +310,28 @@ __global__ __launch_bounds__(V_THREADS, 2) void gemm_nvfp4_pipe_ksplit64_kernel(
   nv_ksplit_block<64>(x, w, sp, y, M, N, K, S, part);
 }
 
-// The split tiles' results: block b sums wave b % 8's accumulators of tile b / 8 over its S
-// K ranges (in K order) and stores them to y as bf16, as the tile epilogue does.
+// The split tiles' results: one thread per float4 of a tile's partial layout
+// (gp_reduce_quad), 8 * FI * FJ * 4 * 64 threads per tile, nv_reduce_blocks<TM> blocks of 256.
 template <int TM>
-__global__ __launch_bounds__(64) void gemm_nvfp4_split_reduce_kernel(const float *__restrict__ part,
-                                                                      uint16_t *__restrict__ y, int M, int N, int S) {
+constexpr int nv_reduce_blocks() {
+  return TM == 64 ? 2 * 2 * 1 * 4 : 2 * (TM / 64) * 2 * 4;  // 2 * FI * FJ * 4
+}
+template <int TM>
+__global__ __launch_bounds__(256) void gemm_nvfp4_split_reduce_kernel(const float *__restrict__ part,
+                                                                       uint16_t *__restrict__ y, int M, int N, int S) {
   // the wave layout of nv_tile<TM>
   constexpr bool COLS = TM == 64;
   constexpr int FI = COLS ? 2 : TM / 64, FJ = COLS ? 1 : 2;
   constexpr int WM = COLS ? TM : TM / 2, WN = 32 * FJ;
-  constexpr int REGION = 32 * FI * (64 * FJ + 32);
-  __shared__ __attribute__((aligned(16))) uint8_t region[REGION];
-  const int t = blockIdx.x >> 3, wave = blockIdx.x & 7, lane = threadIdx.x;
+  constexpr int NQ = FI * FJ * 4;  // float4s per lane per wave
+  static_assert(8 * NQ * 64 == 256 * nv_reduce_blocks<TM>(), "whole blocks per tile");
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  const int t = g / (8 * NQ * 64), rem = g - t * (8 * NQ * 64);
+  const int wave = rem / (NQ * 64), q = (rem >> 6) % NQ, lane = rem & 63;
   int tm, tn;
   tile_of(t, (M + TM - 1) / TM, (N + V_BN - 1) / V_BN, &tm, &tn);
   const int wm = COLS ? 0 : wave & 1, wn = COLS ? wave : wave >> 1;
-  f32x16_t acc[FI][FJ];
-  gp_sum_partials<FI, FJ>(acc, part, t, S, wave, lane, M - (tm * TM + wm * WM));
-  const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
-  gp_store_tile_bf16<FI, FJ, 0, FI>(acc, region, lane, y, M, N, tm * TM + wm * WM, tn * V_BN + wn * WN, N, vec);
+  gp_reduce_quad<FI, FJ>(part, y, M, N, N, t, S, wave, q, lane, tm * TM + wm * WM, tn * V_BN + wn * WN);
 }
 
 // Both tile heights in one launch: blocks [0, tiles1) are the 256-row tiles of W rows
@@ -400,22 +411,22 @@ hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
                          (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, sp.S, part);
       e = hipGetLastError();
       if (e == hipSuccess)
-        hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<64>, dim3(sp.tiles * 8), dim3(64), 0, st,
-                           (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
+        hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<64>, dim3(sp.tiles * nv_reduce_blocks<64>()), dim3(256), 0,
+                           st, (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
     } else if (sp.TM == 128) {
       hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit_kernel<128>, dim3(blocks), dim3(V_THREADS), V_LDS, st,
                          (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, sp.S, part);
       e = hipGetLastError();
       if (e == hipSuccess)
-        hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<128>, dim3(sp.tiles * 8), dim3(64), 0, st,
-                           (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
+        hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<128>, dim3(sp.tiles * nv_reduce_blocks<128>()), dim3(256), 0,
+                           st, (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
     } else {
       hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit_kernel<256>, dim3(blocks), dim3(V_THREADS), V_LDS, st,
                          (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, sp.S, part);
       e = hipGetLastError();
       if (e == hipSuccess)
-        hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<256>, dim3(sp.tiles * 8), dim3(64), 0, st,
-                           (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
+        hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<256>, dim3(sp.tiles * nv_reduce_blocks<256>()), dim3(256), 0,
+                           st, (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
     }
     return e == hipSuccess ? hipGetLastError() : e;
   }

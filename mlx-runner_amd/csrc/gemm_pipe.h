@@ -144,32 +144,35 @@ __device__ __forceinline__ void gp_store_partial(const f32x16_t (&acc)[FI][FJ], 
   }
 }
 
-// One wave's accumulators of split tile t summed over its S slots (t S .. t S + S - 1) in K
-// order, the same order whichever block finished first, so the result is deterministic.
+// The split-tile reduce, one thread per float4 of the partial layout: float4 (wave, q, lane)
+// of split tile t, q = (i FJ + j) 4 + v4, is summed over the tile's S <= GP_MAX_SPLIT slots
+// (t S .. t S + S - 1) in K order, the same order whichever block finished first, so the
+// result is deterministic.  Its four values are rows 32 i + 8 v4 + 4 (lane / 32) + [0, 4),
+// column 32 j + lane % 32 of the wave's region at (row0, col0) of y; they are rounded to bf16
+// as the tile epilogue rounds (rows from M on and columns from col_end on are not stored).
+// All S loads are issued before the first add, so a thread waits for one round trip, not S.
+constexpr int GP_MAX_SPLIT = 8;
 template <int FI, int FJ>
-__device__ __forceinline__ void gp_sum_partials(f32x16_t (&acc)[FI][FJ], const float *__restrict__ part, int t, int S,
-                                                int wave, int lane, int live_rows) {
+__device__ __forceinline__ void gp_reduce_quad(const float *__restrict__ part, uint16_t *__restrict__ y, int M, int N,
+                                               int col_end, int t, int S, int wave, int q, int lane, int row0,
+                                               int col0) {
+  const int i = q / (FJ * 4), j = (q / 4) % FJ, v4 = q % 4;
+  const int r = row0 + 32 * i + 8 * v4 + 4 * (lane >> 5), c = col0 + 32 * j + (lane & 31);
+  if (r >= M || c >= col_end) return;  // not stored by the split blocks either (rows past M)
+  const float4 *pw = (const float4 *)part + ((size_t)t * S * 8 + wave) * FI * FJ * 4 * 64 + q * 64 + lane;
+  const size_t slot = (size_t)8 * FI * FJ * 4 * 64;  // float4s per slot
+  float4 f[GP_MAX_SPLIT];
 #pragma unroll
-  for (int i = 0; i < FI; ++i)
+  for (int k = 0; k < GP_MAX_SPLIT; ++k) f[k] = pw[(k < S ? k : S - 1) * slot];
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int j = 0; j < FJ; ++j)
+  for (int k = 0; k < GP_MAX_SPLIT; ++k)
+    if (k < S) s.x += f[k].x, s.y += f[k].y, s.z += f[k].z, s.w += f[k].w;
+  const float v[4] = {s.x, s.y, s.z, s.w};
+  uint16_t *dst = y + (int64_t)r * N + c;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-  for (int k = 0; k < S; ++k) {
-    const float4 *pw = (const float4 *)part + ((size_t)(t * S + k) * 8 + wave) * FI * FJ * 4 * 64 + lane;
-    float4 f[FI * FJ * 4];
-#pragma unroll
-    for (int q = 0; q < FI * FJ * 4; ++q)
-      f[q] = 32 * (q / (FJ * 4)) < live_rows ? pw[q * 64] : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int q = 0; q < FI * FJ * 4; ++q) {
-      const int i = q / (FJ * 4), j = (q / 4) % FJ, v4 = q % 4;
-      acc[i][j][4 * v4] += f[q].x;
-      acc[i][j][4 * v4 + 1] += f[q].y;
-      acc[i][j][4 * v4 + 2] += f[q].z;
-      acc[i][j][4 * v4 + 3] += f[q].w;
-    }
-  }
+  for (int e = 0; e < 4; ++e)
+    if (r + e < M) dst[(int64_t)e * N] = __builtin_bit_cast(uint16_t, (__bf16)v[e]);
 }
 
 // Weight scales [N, nb bytes] (row-major, as loaded) -> tile-major: for each
