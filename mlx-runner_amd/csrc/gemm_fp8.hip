@@ -696,7 +696,7 @@ size_t gemm_mxfp8_workspace(const QmmArgs &a) {
 size_t tiled_scales_bytes(int64_t N, int nb) { return (size_t)round256((size_t)N) * (size_t)nb; }
 
 int gemm_tiled_scale_bytes_per_row(const QmmArgs &a) {
-  if (a.M <= QMV_MAX_M || a.x_f32 || a.K <= 0) return 0;
+  if (qmm_on_decode(a) || a.x_f32 || a.K <= 0) return 0;
   if (gemm_mxfp8_ok(a)) return gemm_mxfp8_pipe_ok(a) && (uintptr_t)a.x % 16 == 0 ? a.K / 32 : 0;
   if (gemm_nvfp4_ok(a)) return a.K / 16;
   return 0;

@@ -572,7 +572,7 @@ static int tiled_scales(Arr *sa, const QmmArgs &a, hipStream_t st, const uint32_
 
 // Workspace bytes run_qmm needs for these arguments (0 for the decode kernels).
 static size_t qmm_workspace(const QmmArgs &a) {
-  if (a.M <= QMV_MAX_M || a.K == 0 || (((uintptr_t)a.x | (uintptr_t)a.w) & 15) != 0) return 0;
+  if (qmm_on_decode(a) || a.K == 0 || (((uintptr_t)a.x | (uintptr_t)a.w) & 15) != 0) return 0;
   if (gemm_mxfp8_ok(a)) return gemm_mxfp8_workspace(a);
   if (gemm_nvfp4_ok(a)) return gemm_nvfp4_workspace(a);
   return 0;
@@ -588,7 +588,7 @@ static int run_qmm(QmmArgs &a, size_t ybytes, hipStream_t st, const char *op, vo
   hipError_t e = hipSuccess;
   if (K == 0) {
     e = launch_fill_zero(a.y, ybytes, st);
-  } else if (a.M <= QMV_MAX_M) {
+  } else if (qmm_on_decode(a)) {
     if (qmv_mfma_ok(a))
       e = launch_qmv_mfma(a, st);
     else

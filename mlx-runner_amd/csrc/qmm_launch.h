@@ -87,7 +87,7 @@ bool qmv_mlp_ok(const QmmArgs &a);
 hipError_t launch_qmv_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st);
 hipError_t launch_silu_mul(const void *g, const void *u, void *h, int64_t n, bool f32, hipStream_t st);
 
-// Prefill GEMM (M > QMV_MAX_M).
+// Prefill GEMM (M > QMV_MAX_M, and nvfp4 at 5-8 rows: qmm_on_decode).
 bool gemm_ok(const QmmArgs &a);
 hipError_t launch_gemm(const QmmArgs &a, hipStream_t st);
 
@@ -109,6 +109,19 @@ hipError_t launch_repack_scales(const uint8_t *s, int64_t N, int nb, uint32_t *o
 // Whether the prefill GEMM for these arguments reads tile-major scales (and how many
 // scale bytes per row it repacks): 0 when it reads them as stored.
 int gemm_tiled_scale_bytes_per_row(const QmmArgs &a);
+
+// Whether a call runs on the decode kernels (x of at most QMV_MAX_M rows) rather than a
+// prefill GEMM.  x of 5-8 rows that the MFMA decode kernels do not take (nvfp4; mxfp8 at
+// K = 17408 from 6 rows) runs on the pipelined GEMM's split tiles when the matrix is tall:
+// the other decode kernel is the unpacking GEMV, whose work grows with every row
+// (N = 17408, K = 5120, nvfp4: 40-62 us at 5-8 rows against 25 us; N = 5120, K = 17408,
+// mxfp8: 50-61 us against 47 us).
+inline bool qmm_on_decode(const QmmArgs &a) {
+  if (a.M > QMV_MAX_M) return false;
+  if (a.M <= 4 || a.N < 4096 || qmv_mfma_ok(a) || ((uintptr_t)a.x | (uintptr_t)a.w) & 15) return true;
+  if (a.mode == MXFP8) return !(gemm_mxfp8_ok(a) && a.K % 128 == 0 && ((uintptr_t)a.s & 3) == 0);
+  return !gemm_nvfp4_ok(a);
+}
 
 // dequant: out [N, K] float32 (out_f32) or bfloat16.
 hipError_t launch_dequant(int mode, const uint8_t *w, const uint8_t *s, int64_t N, int64_t K, void *out,

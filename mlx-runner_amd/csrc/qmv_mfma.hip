@@ -44,6 +44,8 @@ namespace qmm {
 namespace {
 
 constexpr int QF_REC = 272;  // x record of one (x row, 128-K chunk): 256 data bytes, then 16 zero bytes
+// x rows the record area of a wave's tile is laid out for: 4, or M when more (mxfp8, M <= 8)
+constexpr int qf_rec_rows(int M) { return M > 4 ? M : 4; }
 constexpr int QF_FLUSH_MAX = 16;
 
 // Keeps a value in its own register until this point.  The scale operands of
@@ -113,7 +115,7 @@ __device__ __forceinline__ void split8(const uint4 q, uint2 &hi, uint2 &lo, int 
 //          (m, hi|lo, c, block) at 64 m + (4 hl + c) * 4 + block.
 template <int MODE, int M>
 __device__ __forceinline__ void qf_write_records(uint8_t *tile, const uint4 (&xin)[M], int lane) {
-  uint8_t *ex = tile + 4 * 4 * QF_REC;
+  uint8_t *ex = tile + 4 * qf_rec_rows(M) * QF_REC;
   const int c = lane >> 4, kc = (lane & 15) * 8;  // chunk of the slice, offset in the chunk
 #pragma unroll
   for (int m = 0; m < M; ++m) {
@@ -155,20 +157,21 @@ __device__ __forceinline__ int rows_begin(int b, int rbase, int rrem) { return b
 // stream HBM well; the MFMA operand layout (16 rows x 64 bytes per instruction)
 // read straight from HBM does not (measured 6.1-7.0 against 4.8-5.2 TB/s), so
 // each unit passes through the wave's LDS tile to change layout.
-template <int MODE>
+template <int MODE, int M>
 struct QfGeom {
   static constexpr int UB = MODE == NVFP4 ? 256 : 512;  // W bytes per row per unit
   static constexpr int PITCH = UB + 16;                 // tile row pitch: rows land on distinct banks
   static constexpr int LOADS = 16 * UB / 1024;          // 1 KiB loads per unit
   static constexpr int SB = MODE == NVFP4 ? 32 : 16;    // scale bytes per row per unit
   static constexpr int TILE = 16 * PITCH + 16 * SB;
-  static constexpr int PREP = 4 * 4 * QF_REC + 4 * 64;  // x records (M <= 4 rows x 4 chunks) + exponents
+  static constexpr int PREP = qf_rec_rows(M) * (4 * QF_REC + 64);  // x records (rows x 4 chunks) + exponents
   static constexpr int WAVE_LDS = TILE > PREP ? TILE : PREP;
 };
 
 template <int MODE>
 constexpr size_t qf_lds_bytes(int M, int Q, int F) {
-  return (size_t)Q * QfGeom<MODE>::WAVE_LDS + (size_t)F * M * Q * 16 * 4;
+  const size_t prep = (size_t)qf_rec_rows(M) * (4 * QF_REC + 64), tile = QfGeom<MODE, 1>::TILE;
+  return (size_t)Q * (tile > prep ? tile : prep) + (size_t)F * M * Q * 16 * 4;
 }
 
 // NMAT = 2 is the MLP form (src/model.zig:905-915): a unit's 16 MFMA columns
@@ -190,7 +193,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
                                                           const uint8_t *__restrict__ w,
                                                           const uint8_t *__restrict__ s, const uint8_t *__restrict__ w2,
                                                           const uint8_t *__restrict__ s2, const YOut yo) {
-  using G = QfGeom<MODE>;
+  using G = QfGeom<MODE, M>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
   uint8_t *tile = lds + q * G::WAVE_LDS;
@@ -269,7 +272,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
   // 3) x split into records in this wave's tile (before it holds weights), then the
   //    A operands of the slice's 4 chunks into registers, kept for the pass.
   //    E4M3 A layout: lane group h, byte t holds logical K 64 (t/16) + 16 h + t%16.
-  uint8_t *ex = tile + 4 * 4 * QF_REC;  // exponent bytes, 64 per x row
+  uint8_t *ex = tile + 4 * qf_rec_rows(M) * QF_REC;  // exponent bytes, 64 per x row
   const int h = lane >> 4, n = lane & 15;
   constexpr int MA = MODE == NVFP4 ? M : 1;  // A operands per chunk
   i32x8_t areg[4][MA];
@@ -670,7 +673,8 @@ static int qf_flush_rows(const QmmArgs &a, int nrb) {
 static bool q32_ok(const QmmArgs &a);
 
 bool qmv_mfma_ok(const QmmArgs &a) {
-  if (a.x_f32 || a.M < 1 || a.N < 16 || a.M > 4) return false;
+  // (mxfp8 holds x rows as A columns (m, hi|lo): 16 columns, up to 8 rows)
+  if (a.x_f32 || a.M < 1 || a.N < 16 || a.M > (a.mode == MXFP8 ? 8 : 4)) return false;
   // nvfp4 at M = 3-4 runs the 32x32x64 form (the 16x16x128 form's A operands would
   // not fit in registers); measured faster than the unpacking GEMV from N = 4096
   // (N = 5120, K = 5120, M = 3: 7.8 against 9.4 us; gate+up M = 3: 22.8 against 30.7;
@@ -678,6 +682,7 @@ bool qmv_mfma_ok(const QmmArgs &a) {
   if (a.mode == NVFP4 && a.M > 2) return a.N >= 4096 && q32_ok(a);
   const QfShape g = qf_shape(a.K);
   if (g.Q == 0) return false;
+  if (a.M > 5 && g.P == 3) return false;  // x of three passes for 6-8 rows would not fit in registers
   // Where this path is faster than the unpacking GEMV (measured on the 256-CU
   // MI355X): at M = 1 only for nvfp4, with many rows per CU at K = 5120 (it pays
   // a per-workgroup x split and pipeline fill) and at K = 17408 (N = 5120: 11.8
@@ -700,7 +705,7 @@ static bool q32_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_u
 // The fused MLP form: the 16x16x128 kernel (nvfp4 M <= 2, mxfp8 M <= 4) and the
 // 32x32x64 kernel at one pass (nvfp4 M = 3-4, K = 5120).
 bool qmv_mfma_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up) {
-  if (!qmv_mfma_ok(a) || a.K != 5120) return false;
+  if (!qmv_mfma_ok(a) || a.K != 5120 || a.M > 4) return false;
   if (a.mode == NVFP4 && a.M > 2) return q32_mlp_ok(a, w_up, s_up);
   return (((uintptr_t)w_up) & 15) == 0 && (((uintptr_t)s_up) & 7) == 0;
 }
@@ -728,7 +733,10 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
                               hipStream_t st) {
   if constexpr (NMAT == 1 && !PARTS) {
     const QfShape g = qf_shape(a.K);
-    if (g.P == 3) return launch_qf<MODE, M, 12, 1, 1, 3>(a, w2, s2, grid, F, st);
+    if (g.P == 3) {
+      if constexpr (M <= 5) return launch_qf<MODE, M, 12, 1, 1, 3>(a, w2, s2, grid, F, st);
+      return hipErrorInvalidValue;  // (qmv_mfma_ok: x of three passes would not fit in registers)
+    }
     if (g.P == 2) return launch_qf<MODE, M, 10, 1, 1, 2>(a, w2, s2, grid, F, st);
     if (g.Q == 12) return launch_qf<MODE, M, 12, 1, 1, 1>(a, w2, s2, grid, F, st);
   }
@@ -750,6 +758,15 @@ static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8
   if (a.mode == NVFP4) {
     if (a.M == 1) return launch_qf_d<NVFP4, 1, NMAT, PARTS>(a, w2, s2, grid, F, nrb, st);
     return launch_qf_d<NVFP4, 2, NMAT, PARTS>(a, w2, s2, grid, F, nrb, st);
+  }
+  if constexpr (NMAT == 1 && !PARTS) {  // (grouped calls and the MLP form run M <= 4)
+    switch (a.M) {
+      case 5: return launch_qf_d<MXFP8, 5, 1>(a, w2, s2, grid, F, nrb, st);
+      case 6: return launch_qf_d<MXFP8, 6, 1>(a, w2, s2, grid, F, nrb, st);
+      case 7: return launch_qf_d<MXFP8, 7, 1>(a, w2, s2, grid, F, nrb, st);
+      case 8: return launch_qf_d<MXFP8, 8, 1>(a, w2, s2, grid, F, nrb, st);
+      default: break;
+    }
   }
   switch (a.M) {
     case 1: return launch_qf_d<MXFP8, 1, NMAT, PARTS>(a, w2, s2, grid, F, nrb, st);
