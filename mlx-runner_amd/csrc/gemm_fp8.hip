@@ -371,7 +371,7 @@ template <int TS>
 __device__ __forceinline__ void pipe_tile(int bid, const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl,
                                           const uint8_t *__restrict__ sh, const uint8_t *__restrict__ sl,
                                           const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
-                                          uint16_t *__restrict__ y, int M, int N, int K, int n_begin, int n_end,
+                                          const YOut yo, int M, int N, int K, int n_begin, int n_end,
                                           int s_begin, int s_end, float *__restrict__ part) {
   using G = PipeGeom<TS>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -533,8 +533,8 @@ __device__ __forceinline__ void pipe_tile(int bid, const uint8_t *__restrict__ x
   // after which no fragment read or DMA is outstanding); wave w's region follows w - 1's
   constexpr int REGION = 32 * G::FI * (64 * G::FJ + 32);
   static_assert(8 * REGION <= G::LDS, "the epilogue regions fit the ring");
-  const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
-  gp_store_tile_bf16<G::FI, G::FJ, 0, G::FI>(acc, lds + wave * REGION, lane, y, M, N, m0 + wm * (TS / 4),
+  const bool vec = yout_vec(yo);
+  gp_store_tile_bf16<G::FI, G::FJ, 0, G::FI>(acc, lds + wave * REGION, lane, yo, M, m0 + wm * (TS / 4),
                                              n0 + wn * (TS / 2), n_end, vec);
 }
 
@@ -543,8 +543,8 @@ template <int TS>
 __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
     const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
     const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
-    uint16_t *__restrict__ y, int M, int N, int K, int n_begin, int n_end) {
-  pipe_tile<TS>(blockIdx.x, xh, xl, sh, sl, w, sw, y, M, N, K, n_begin, n_end, 0, K / P_BK, nullptr);
+    const YOut yo, int M, int N, int K, int n_begin, int n_end) {
+  pipe_tile<TS>(blockIdx.x, xh, xl, sh, sl, w, sw, yo, M, N, K, n_begin, n_end, 0, K / P_BK, nullptr);
 }
 
 // Both tilings in one launch: blocks [0, tiles1) are the 256-tiles of W rows [0, n_split),
@@ -561,15 +561,15 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_kernel(
 __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_split_kernel(
     const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
     const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
-    uint16_t *__restrict__ y, int M, int N, int K, int n_split, int tiles1, int S, float *__restrict__ part) {
+    const YOut yo, int M, int N, int K, int n_split, int tiles1, int S, float *__restrict__ part) {
   const int b = blockIdx.x, steps = K / P_BK;
   if (b < tiles1) {
-    pipe_tile<256>(b, xh, xl, sh, sl, w, sw, y, M, N, K, 0, n_split, 0, steps, nullptr);
+    pipe_tile<256>(b, xh, xl, sh, sl, w, sw, yo, M, N, K, 0, n_split, 0, steps, nullptr);
   } else if (S == 0) {
-    pipe_tile<128>(b - tiles1, xh, xl, sh, sl, w, sw, y, M, N, K, n_split, N, 0, steps, nullptr);
+    pipe_tile<128>(b - tiles1, xh, xl, sh, sl, w, sw, yo, M, N, K, n_split, N, 0, steps, nullptr);
   } else {
     const int u = b - tiles1, t = u / S, k = u - t * S;
-    pipe_tile<256>(t, xh, xl, sh, sl, w, sw, y, M, N, K, n_split, N, k * steps / S, (k + 1) * steps / S,
+    pipe_tile<256>(t, xh, xl, sh, sl, w, sw, yo, M, N, K, n_split, N, k * steps / S, (k + 1) * steps / S,
                    part + (size_t)u * 256 * 256);
   }
 }
@@ -580,9 +580,9 @@ __global__ __launch_bounds__(F_THREADS) void gemm_mxfp8_pipe_split_kernel(
 __global__ __launch_bounds__(F_THREADS, 2) void gemm_mxfp8_pipe_ksplit128_kernel(
     const uint8_t *__restrict__ xh, const uint8_t *__restrict__ xl, const uint8_t *__restrict__ sh,
     const uint8_t *__restrict__ sl, const uint8_t *__restrict__ w, const uint8_t *__restrict__ sw,
-    uint16_t *__restrict__ y, int M, int N, int K, int S, float *__restrict__ part) {
+    const YOut yo, int M, int N, int K, int S, float *__restrict__ part) {
   const int b = blockIdx.x, t = b / S, k = b - t * S, steps = K / P_BK;
-  pipe_tile<128>(t, xh, xl, sh, sl, w, sw, y, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S,
+  pipe_tile<128>(t, xh, xl, sh, sl, w, sw, yo, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S,
                  part + (size_t)b * 128 * 128);
 }
 
@@ -594,7 +594,7 @@ constexpr int fp8_reduce_blocks() {
 }
 template <int TS>
 __global__ __launch_bounds__(256) void gemm_mxfp8_split_reduce_kernel(const float *__restrict__ part,
-                                                                       uint16_t *__restrict__ y, int M, int N,
+                                                                       const YOut yo, int M, int N,
                                                                        int n_split, int S) {
   using G = PipeGeom<TS>;
   constexpr int NQ = G::FI * G::FJ * 4;  // float4s per lane per wave
@@ -605,7 +605,7 @@ __global__ __launch_bounds__(256) void gemm_mxfp8_split_reduce_kernel(const floa
   int tm, tn;
   tile_of(t, (M + TS - 1) / TS, (N - n_split + TS - 1) / TS, &tm, &tn);
   const int wm = wave >> 1, wn = wave & 1;
-  gp_reduce_quad<G::FI, G::FJ>(part, y, M, N, N, t, S, wave, q, lane, tm * TS + wm * (TS / 4),
+  gp_reduce_quad<G::FI, G::FJ>(part, yo, M, N, t, S, wave, q, lane, tm * TS + wm * (TS / 4),
                                n_split + tn * TS + wn * (TS / 2));
 }
 
@@ -746,15 +746,16 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
     // One block per CU at a time (the ring fills most of a CU's LDS); see fp8_plan for
     // how the last partial round runs.
     const Fp8Plan p = fp8_plan(a, cus);
+    const YOut yo = yout_of(a);  // y, or a grouped call's parts
     if (p.n_split == a.N) {
       hipLaunchKernelGGL(gemm_mxfp8_pipe_kernel<256>, dim3(p.tiles1), dim3(F_THREADS), PipeGeom<256>::LDS, st, xh, xl,
-                         sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, 0, a.N);
+                         sh, sl, a.w, swp, yo, a.M, a.N, a.K, 0, a.N);
       return hipGetLastError();
     }
     if (p.S == 0) {
       const int tiles2 = ((a.M + 127) / 128) * ((a.N - p.n_split + 127) / 128);
       hipLaunchKernelGGL(gemm_mxfp8_pipe_split_kernel, dim3(p.tiles1 + tiles2), dim3(F_THREADS), PipeGeom<256>::LDS,
-                         st, xh, xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, p.n_split, p.tiles1, 0,
+                         st, xh, xl, sh, sl, a.w, swp, yo, a.M, a.N, a.K, p.n_split, p.tiles1, 0,
                          (float *)nullptr);
       return hipGetLastError();
     }
@@ -766,22 +767,23 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
       e = ensure_dynamic_lds(lds128, (const void *)gemm_mxfp8_pipe_ksplit128_kernel, (int)PipeGeom<128>::LDS);
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(gemm_mxfp8_pipe_ksplit128_kernel, dim3(p.tail_tiles * p.S), dim3(F_THREADS),
-                         PipeGeom<128>::LDS, st, xh, xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, p.S, part);
+                         PipeGeom<128>::LDS, st, xh, xl, sh, sl, a.w, swp, yo, a.M, a.N, a.K, p.S, part);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel<128>, dim3(p.tail_tiles * fp8_reduce_blocks<128>()), dim3(256), 0,
-                         st, (const float *)part, (uint16_t *)a.y, a.M, a.N, 0, p.S);
+                         st, (const float *)part, yo, a.M, a.N, 0, p.S);
       return hipGetLastError();
     }
     hipLaunchKernelGGL(gemm_mxfp8_pipe_split_kernel, dim3(p.tiles1 + p.tail_tiles * p.S), dim3(F_THREADS),
-                       PipeGeom<256>::LDS, st, xh, xl, sh, sl, a.w, swp, (uint16_t *)a.y, a.M, a.N, a.K, p.n_split,
+                       PipeGeom<256>::LDS, st, xh, xl, sh, sl, a.w, swp, yo, a.M, a.N, a.K, p.n_split,
                        p.tiles1, p.S, part);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel<256>, dim3(p.tail_tiles * fp8_reduce_blocks<256>()), dim3(256), 0,
-                       st, (const float *)part, (uint16_t *)a.y, a.M, a.N, p.n_split, p.S);
+                       st, (const float *)part, yo, a.M, a.N, p.n_split, p.S);
     return hipGetLastError();
   }
+  if (a.parts) return hipErrorInvalidValue;  // (grouped calls run the pipelined kernels only)
   static std::atomic<uint64_t> lds_set{0};
   e = ensure_dynamic_lds(lds_set, (const void *)gemm_mxfp8_kernel, (int)sizeof(Fp8Smem));
   if (e != hipSuccess) return e;

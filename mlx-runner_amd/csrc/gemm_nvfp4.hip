@@ -85,7 +85,7 @@ __device__ __forceinline__ bf16x8_t deq8_nvfp4(uint32_t word, uint32_t scale_byt
 // accumulators go to `part` (gp_store_partial's layout).
 template <int TM>
 __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x, const uint8_t *__restrict__ w,
-                                        const uint8_t *__restrict__ sp, uint16_t *__restrict__ y, int M, int N, int K,
+                                        const uint8_t *__restrict__ sp, const YOut yo, int M, int N, int K,
                                         int n_begin, int n_end, int s_begin, int s_end, float *__restrict__ part) {
   using G = NvGeom<TM>;
   // Wave layout: 2 (x rows) x 4 (W rows), waves of TM / 2 x 64, or at TM = 64 1 x 8, waves
@@ -266,18 +266,18 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   constexpr int REGION = 32 * NI * (64 * FJ + 32);
   // (the 256- and 128-row instances run with the 256-row ring, the 64-row one with its own)
   static_assert(8 * REGION <= (TM == 64 ? G::LDS : V_LDS), "the epilogue regions fit the launch's ring");
-  const bool vec = N % 8 == 0 && ((uintptr_t)y & 15) == 0;
+  const bool vec = yout_vec(yo);
   uint8_t *region = lds + wave * REGION;
-  gp_store_tile_bf16<FI, FJ, 0, NI>(acc, region, lane, y, M, N, m0 + wm * WM, n0 + wn * WN, n_end, vec);
+  gp_store_tile_bf16<FI, FJ, 0, NI>(acc, region, lane, yo, M, m0 + wm * WM, n0 + wn * WN, n_end, vec);
   if constexpr (FI == 4)
-    gp_store_tile_bf16<FI, FJ, 2, 2>(acc, region, lane, y, M, N, m0 + wm * WM, n0 + wn * WN, n_end, vec);
+    gp_store_tile_bf16<FI, FJ, 2, 2>(acc, region, lane, yo, M, m0 + wm * WM, n0 + wn * WN, n_end, vec);
 }
 
 __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16_t *__restrict__ x,
                                                                     const uint8_t *__restrict__ w,
                                                                     const uint8_t *__restrict__ sp,
-                                                                    uint16_t *__restrict__ y, int M, int N, int K) {
-  nv_tile<256>(blockIdx.x, x, w, sp, y, M, N, K, 0, N, 0, K / V_BK, nullptr);
+                                                                    const YOut yo, int M, int N, int K) {
+  nv_tile<256>(blockIdx.x, x, w, sp, yo, M, N, K, 0, N, 0, K / V_BK, nullptr);
 }
 
 // Every TM x 256 tile split S ways along K: block b runs K range b % S of tile b / S and
@@ -288,26 +288,26 @@ __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_kernel(const uint16
 // at most 128 registers per lane), so a CU keeps two blocks' loads in flight.
 template <int TM>
 __device__ __forceinline__ void nv_ksplit_block(const uint16_t *__restrict__ x, const uint8_t *__restrict__ w,
-                                                const uint8_t *__restrict__ sp, uint16_t *__restrict__ y, int M,
+                                                const uint8_t *__restrict__ sp, const YOut yo, int M,
                                                 int N, int K, int S, float *__restrict__ part) {
   const int b = blockIdx.x, t = b / S, k = b - t * S, steps = K / V_BK;
-  nv_tile<TM>(t, x, w, sp, y, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S, part + (size_t)b * TM * 256);
+  nv_tile<TM>(t, x, w, sp, yo, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S, part + (size_t)b * TM * 256);
 }
 template <int TM>
 __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_ksplit_kernel(const uint16_t *__restrict__ x,
                                                                            const uint8_t *__restrict__ w,
                                                                            const uint8_t *__restrict__ sp,
-                                                                           uint16_t *__restrict__ y, int M, int N,
+                                                                           const YOut yo, int M, int N,
                                                                            int K, int S, float *__restrict__ part) {
-  nv_ksplit_block<TM>(x, w, sp, y, M, N, K, S, part);
+  nv_ksplit_block<TM>(x, w, sp, yo, M, N, K, S, part);
 }
 __global__ __launch_bounds__(V_THREADS, 2) void gemm_nvfp4_pipe_ksplit64_kernel(const uint16_t *__restrict__ x,
                                                                                 const uint8_t *__restrict__ w,
                                                                                 const uint8_t *__restrict__ sp,
-                                                                                uint16_t *__restrict__ y, int M,
+                                                                                const YOut yo, int M,
                                                                                 int N, int K, int S,
                                                                                 float *__restrict__ part) {
-  nv_ksplit_block<64>(x, w, sp, y, M, N, K, S, part);
+  nv_ksplit_block<64>(x, w, sp, yo, M, N, K, S, part);
 }
 
 // The split tiles' results: one thread per float4 of a tile's partial layout
@@ -318,7 +318,7 @@ constexpr int nv_reduce_blocks() {
 }
 template <int TM>
 __global__ __launch_bounds__(256) void gemm_nvfp4_split_reduce_kernel(const float *__restrict__ part,
-                                                                       uint16_t *__restrict__ y, int M, int N, int S) {
+                                                                       const YOut yo, int M, int N, int S) {
   // the wave layout of nv_tile<TM>
   constexpr bool COLS = TM == 64;
   constexpr int FI = COLS ? 2 : TM / 64, FJ = COLS ? 1 : 2;
@@ -331,7 +331,7 @@ __global__ __launch_bounds__(256) void gemm_nvfp4_split_reduce_kernel(const floa
   int tm, tn;
   tile_of(t, (M + TM - 1) / TM, (N + V_BN - 1) / V_BN, &tm, &tn);
   const int wm = COLS ? 0 : wave & 1, wn = COLS ? wave : wave >> 1;
-  gp_reduce_quad<FI, FJ>(part, y, M, N, N, t, S, wave, q, lane, tm * TM + wm * WM, tn * V_BN + wn * WN);
+  gp_reduce_quad<FI, FJ>(part, yo, M, N, t, S, wave, q, lane, tm * TM + wm * WM, tn * V_BN + wn * WN);
 }
 
 // Both tile heights in one launch: blocks [0, tiles1) are the 256-row tiles of W rows
@@ -341,13 +341,13 @@ __global__ __launch_bounds__(256) void gemm_nvfp4_split_reduce_kernel(const floa
 __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_split_kernel(const uint16_t *__restrict__ x,
                                                                           const uint8_t *__restrict__ w,
                                                                           const uint8_t *__restrict__ sp,
-                                                                          uint16_t *__restrict__ y, int M, int N,
+                                                                          const YOut yo, int M, int N,
                                                                           int K, int n_split, int tiles1) {
   const int b = blockIdx.x, steps = K / V_BK;
   if (b < tiles1)
-    nv_tile<256>(b, x, w, sp, y, M, N, K, 0, n_split, 0, steps, nullptr);
+    nv_tile<256>(b, x, w, sp, yo, M, N, K, 0, n_split, 0, steps, nullptr);
   else
-    nv_tile<128>(b - tiles1, x, w, sp, y, M, N, K, n_split, N, 0, steps, nullptr);
+    nv_tile<128>(b - tiles1, x, w, sp, yo, M, N, K, n_split, N, 0, steps, nullptr);
 }
 
 static size_t round256v(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -402,31 +402,32 @@ hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
   if (e == hipSuccess)
     e = ensure_dynamic_lds(lds_k64, (const void *)gemm_nvfp4_pipe_ksplit64_kernel, (int)NvGeom<64>::LDS);
   if (e != hipSuccess) return e;
+  const YOut yo = yout_of(a);  // y, or a grouped call's parts
   const NvSplit sp = nv_split_plan(a, device_cu_count());
   if (sp.S) {
     float *part = (float *)((uint8_t *)ws + round256v(a.s_tiled ? 0 : round256v(a.N) * (size_t)(a.K / 16)));
     const int blocks = sp.tiles * sp.S;
     if (sp.TM == 64) {
       hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit64_kernel, dim3(blocks), dim3(V_THREADS), NvGeom<64>::LDS, st,
-                         (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, sp.S, part);
+                         (const uint16_t *)a.x, a.w, tiled, yo, a.M, a.N, a.K, sp.S, part);
       e = hipGetLastError();
       if (e == hipSuccess)
         hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<64>, dim3(sp.tiles * nv_reduce_blocks<64>()), dim3(256), 0,
-                           st, (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
+                           st, (const float *)part, yo, a.M, a.N, sp.S);
     } else if (sp.TM == 128) {
       hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit_kernel<128>, dim3(blocks), dim3(V_THREADS), V_LDS, st,
-                         (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, sp.S, part);
+                         (const uint16_t *)a.x, a.w, tiled, yo, a.M, a.N, a.K, sp.S, part);
       e = hipGetLastError();
       if (e == hipSuccess)
         hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<128>, dim3(sp.tiles * nv_reduce_blocks<128>()), dim3(256), 0,
-                           st, (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
+                           st, (const float *)part, yo, a.M, a.N, sp.S);
     } else {
       hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit_kernel<256>, dim3(blocks), dim3(V_THREADS), V_LDS, st,
-                         (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, sp.S, part);
+                         (const uint16_t *)a.x, a.w, tiled, yo, a.M, a.N, a.K, sp.S, part);
       e = hipGetLastError();
       if (e == hipSuccess)
         hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<256>, dim3(sp.tiles * nv_reduce_blocks<256>()), dim3(256), 0,
-                           st, (const float *)part, (uint16_t *)a.y, a.M, a.N, sp.S);
+                           st, (const float *)part, yo, a.M, a.N, sp.S);
     }
     return e == hipSuccess ? hipGetLastError() : e;
   }
@@ -441,12 +442,12 @@ hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
   const int tiles1 = tiles_m * ((n_split + V_BN - 1) / V_BN);
   if (n_split == a.N) {
     hipLaunchKernelGGL(gemm_nvfp4_pipe_kernel, dim3(tiles1), dim3(V_THREADS), V_LDS, st, (const uint16_t *)a.x, a.w,
-                       tiled, (uint16_t *)a.y, a.M, a.N, a.K);
+                       tiled, yo, a.M, a.N, a.K);
     return hipGetLastError();
   }
   const int tiles2 = ((a.M + 127) / 128) * ((a.N - n_split + V_BN - 1) / V_BN);
   hipLaunchKernelGGL(gemm_nvfp4_pipe_split_kernel, dim3(tiles1 + tiles2), dim3(V_THREADS), V_LDS, st,
-                     (const uint16_t *)a.x, a.w, tiled, (uint16_t *)a.y, a.M, a.N, a.K, n_split, tiles1);
+                     (const uint16_t *)a.x, a.w, tiled, yo, a.M, a.N, a.K, n_split, tiles1);
   return hipGetLastError();
 }
 

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "qmm_device.h"
+#include "qmm_launch.h"
 
 namespace qmm {
 
@@ -51,8 +52,16 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
 }
 
+// Whether the output parts take 16-byte stores of 8 columns: every part's row length a
+// multiple of 8 (so no 8-column piece crosses a part boundary) and every part 16-byte aligned.
+__device__ __forceinline__ bool yout_vec(const YOut yo) {
+  return ((yo.n0 | yo.n1 | yo.n2 | yo.n3) & 7) == 0 &&
+         (((uintptr_t)yo.y0 | (uintptr_t)yo.y1 | (uintptr_t)yo.y2 | (uintptr_t)yo.y3) & 15) == 0;
+}
+
 // Epilogue of a wave's FI x FJ grid of 32x32 f32 accumulators (rows row0 + [0, 32 FI),
-// cols col0 + [0, 32 FJ) of y[M, N]; columns from col_end on are not this call's), bf16
+// cols col0 + [0, 32 FJ) of y[M, N], whose column c is column c - lo of part yo.at's part
+// (one part: y itself); columns from col_end on are not this call's), bf16
 // out, accumulator blocks i in [I0, I0 + NI).  Element v of lane l of a 32x32 block is
 // row 8 (v / 4) + 4 (l / 32) + v % 4, col l % 32: a store straight from it writes two
 // bytes per lane.  Instead each lane converts its rows 2u, 2u + 1 with one packed RNE
@@ -60,15 +69,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // but keeps its sign), swaps the dword with its neighbour lane (DPP) and keeps one row
 // of the two columns (v_perm: the even lane row 2u, the odd lane row 2u + 1), writes
 // it to the wave's LDS region and reads the region back 16 bytes per lane along rows,
-// so every global store writes 16 contiguous bytes (vec: N % 8 == 0 and y 16-byte
-// aligned; otherwise, and at the last columns, element stores).  The region,
+// so every global store writes 16 contiguous bytes (vec: yout_vec; otherwise, and at the
+// last columns, element stores).  The region,
 // (32 NI) x (64 FJ + 32) bytes, belongs to this wave; the caller guarantees that no
 // other wave reads or writes it meanwhile.
 typedef __bf16 gp_bf16x2_t __attribute__((ext_vector_type(2)));
 template <int FI, int FJ, int I0, int NI>
 __device__ __forceinline__ void gp_store_tile_bf16(const f32x16_t (&acc)[FI][FJ], uint8_t *region, int lane,
-                                                   uint16_t *__restrict__ y, int M, int N, int row0, int col0,
-                                                   int col_end, bool vec) {
+                                                   const YOut yo, int M, int row0, int col0, int col_end,
+                                                   bool vec) {
   constexpr int PITCH = 64 * FJ + 32;  // bytes per region row (the pad spreads a write's rows over the banks)
   const int c = lane & 31, h = lane >> 5;
   const bool odd = c & 1;
@@ -99,7 +108,7 @@ __device__ __forceinline__ void gp_store_tile_bf16(const f32x16_t (&acc)[FI][FJ]
     for (int it = 0; it < NI * 32 / RPI; ++it) {
       const int row = it * RPI + lane / LPR, piece = lane % LPR;
       const uint4 d = *(const uint4 *)(region + row * PITCH + piece * 16);
-      *(uint4 *)(y + (int64_t)(row0 + I0 * 32 + row) * N + col0 + piece * 8) = d;
+      *(uint4 *)yo.at(row0 + I0 * 32 + row, col0 + piece * 8) = d;
     }
     return;
   }
@@ -109,14 +118,13 @@ __device__ __forceinline__ void gp_store_tile_bf16(const f32x16_t (&acc)[FI][FJ]
     const uint4 d = *(const uint4 *)(region + row * PITCH + piece * 16);
     const int gr = row0 + I0 * 32 + row, gc = col0 + piece * 8;
     if (gr < M) {
-      uint16_t *dst = y + (int64_t)gr * N + gc;
       if (vec && gc + 8 <= col_end) {
-        *(uint4 *)dst = d;
+        *(uint4 *)yo.at(gr, gc) = d;
       } else {
         const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          if (gc + e < col_end) dst[e] = (uint16_t)(dw[e >> 1] >> (16 * (e & 1)));
+          if (gc + e < col_end) *yo.at(gr, gc + e) = (uint16_t)(dw[e >> 1] >> (16 * (e & 1)));
       }
     }
   }
@@ -148,14 +156,13 @@ __device__ __forceinline__ void gp_store_partial(const f32x16_t (&acc)[FI][FJ], 
 // of split tile t, q = (i FJ + j) 4 + v4, is summed over the tile's S <= GP_MAX_SPLIT slots
 // (t S .. t S + S - 1) in K order, the same order whichever block finished first, so the
 // result is deterministic.  Its four values are rows 32 i + 8 v4 + 4 (lane / 32) + [0, 4),
-// column 32 j + lane % 32 of the wave's region at (row0, col0) of y; they are rounded to bf16
+// column 32 j + lane % 32 of the wave's region at (row0, col0) of y (yo.at); they are rounded to bf16
 // as the tile epilogue rounds (rows from M on and columns from col_end on are not stored).
 // All S loads are issued before the first add, so a thread waits for one round trip, not S.
 constexpr int GP_MAX_SPLIT = 8;
 template <int FI, int FJ>
-__device__ __forceinline__ void gp_reduce_quad(const float *__restrict__ part, uint16_t *__restrict__ y, int M, int N,
-                                               int col_end, int t, int S, int wave, int q, int lane, int row0,
-                                               int col0) {
+__device__ __forceinline__ void gp_reduce_quad(const float *__restrict__ part, const YOut yo, int M, int col_end,
+                                               int t, int S, int wave, int q, int lane, int row0, int col0) {
   const int i = q / (FJ * 4), j = (q / 4) % FJ, v4 = q % 4;
   const int r = row0 + 32 * i + 8 * v4 + 4 * (lane >> 5), c = col0 + 32 * j + (lane & 31);
   if (r >= M || c >= col_end) return;  // not stored by the split blocks either (rows past M)
@@ -169,10 +176,9 @@ __device__ __forceinline__ void gp_reduce_quad(const float *__restrict__ part, u
   for (int k = 0; k < GP_MAX_SPLIT; ++k)
     if (k < S) s.x += f[k].x, s.y += f[k].y, s.z += f[k].z, s.w += f[k].w;
   const float v[4] = {s.x, s.y, s.z, s.w};
-  uint16_t *dst = y + (int64_t)r * N + c;
 #pragma unroll
   for (int e = 0; e < 4; ++e)
-    if (r + e < M) dst[(int64_t)e * N] = __builtin_bit_cast(uint16_t, (__bf16)v[e]);
+    if (r + e < M) *yo.at(r + e, c) = __builtin_bit_cast(uint16_t, (__bf16)v[e]);
 }
 
 // Weight scales [N, nb bytes] (row-major, as loaded) -> tile-major: for each

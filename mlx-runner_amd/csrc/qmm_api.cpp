@@ -570,6 +570,14 @@ static int tiled_scales(Arr *sa, const QmmArgs &a, hipStream_t st, const uint32_
   return 0;
 }
 
+// Whether a grouped call's stacked matrices can run as one prefill GEMM: the pipelined
+// kernels (mxfp8: K % 128, scales 4-byte aligned), whose epilogues store to parts.
+static bool gemm_parts_ok(const QmmArgs &a) {
+  if (a.x_f32 || (((uintptr_t)a.x | (uintptr_t)a.w) & 15) != 0) return false;
+  if (a.mode == MXFP8) return gemm_mxfp8_ok(a) && a.K % 128 == 0 && ((uintptr_t)a.s & 3) == 0;
+  return gemm_nvfp4_ok(a);
+}
+
 // Workspace bytes run_qmm needs for these arguments (0 for the decode kernels).
 static size_t qmm_workspace(const QmmArgs &a) {
   if (qmm_on_decode(a) || a.K == 0 || (((uintptr_t)a.x | (uintptr_t)a.w) & 15) != 0) return 0;
@@ -741,6 +749,14 @@ int qmm_quantized_matmul_group(qmm_array *res, size_t n, qmm_array x, const qmm_
     if (qmv_parts_ok(a)) {
       const hipError_t e = qmv_mfma_ok(a) ? launch_qmv_mfma(a, st) : launch_qmv(a, st);
       if (e != hipSuccess) return finish(fail_hip(e, op));
+      g_group_launches.fetch_add(1, std::memory_order_relaxed);
+      return finish(0);
+    }
+    // prefill shapes: one GEMM over the stacked matrices (one x split, one tiling of all
+    // their rows, so narrow members share rounds with the wide ones), each output column
+    // stored to its part.  The scales are repacked per call (no handle holds the stack's).
+    if (!qmm_on_decode(a) && gemm_parts_ok(a)) {
+      if (run_qmm(a, 0, st, op)) return finish(1);
       g_group_launches.fetch_add(1, std::memory_order_relaxed);
       return finish(0);
     }

@@ -10,6 +10,8 @@ them as one matrix when they lie back to back in memory.  Checks:
     parts of 3..1000 rows);
   * where the one launch and the single calls pick the same kernel family, the
     grouped parts equal the single calls bit for bit;
+  * at prefill sizes one GEMM over the stacked matrices, whose epilogue and split-tile
+    reduce store each column to its part;
   * the loader places a layer's group back to back across shards, and
     named_linear_q_group on it equals named_linear_q per name.
 """
@@ -143,14 +145,53 @@ def test_group_same_kernel_bit_exact(mode, M):
 
 
 @pytest.mark.parametrize("mode", ["nvfp4", "mxfp8"])
-def test_group_prefill_runs_per_matrix(mode):
-    """M > 4: each matrix through its own GEMM; results at the qmm bar."""
+def test_group_prefill_one_gemm(mode):
+    """M > 4: one prefill GEMM over the stacked matrices, each part's columns stored to
+    that part; results at the qmm bar."""
     rows, K, M = (256, 64, 32), 512, 40
     keep, arrs, host = device_group(mode, rows, K, seed=13)
     xb = bf16(np.random.default_rng(9).standard_normal((M, K)))
+    before = Q.lib.qmm_group_launch_count()
     outs = Q.quantized_matmul_group(Q.Array.from_numpy(xb, Q.BFLOAT16), [a[0] for a in arrs],
                                     [a[1] for a in arrs], mode)
+    assert Q.lib.qmm_group_launch_count() == before + 1
     check_parts(mode, xb, outs, host, "prefill")
+
+
+# The model's groups at prefill sizes: M = 16 and 96 run split tiles (each tile's K over
+# several blocks, then the reduce stores to the parts), M = 300 whole tiles with a partial
+# last round (mxfp8: 128-tiles in the same launch; nvfp4: 128-row tiles).  Parts whose
+# rows are not a multiple of 8 (ragged) take element stores throughout.
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp8"])
+@pytest.mark.parametrize("group,M", [("gdn_in_proj", 16), ("gdn_in_proj", 300), ("attn_qkv", 96),
+                                     ("attn_qkv", 300), ("ragged_small", 64), ("ragged_big", 200)])
+def test_group_prefill_model_shapes(mode, group, M):
+    rows, K = GROUPS[group], 5120
+    print(f"group {group} {mode} M={M}", flush=True)
+    keep, arrs, host = device_group(mode, rows, K, seed=sorted(GROUPS).index(group))
+    xb = bf16(np.random.default_rng(100 + M).standard_normal((M, K)))
+    x = Q.Array.from_numpy(xb, Q.BFLOAT16)
+    before = Q.lib.qmm_group_launch_count()
+    outs = Q.quantized_matmul_group(x, [a[0] for a in arrs], [a[1] for a in arrs], mode)
+    assert Q.lib.qmm_group_launch_count() == before + 1
+    # every part at the qmm bar on a row and column sample, against the oracle and against
+    # the part's own single call (a different tiling of the same sums)
+    rs = np.unique(np.r_[0:M:max(1, M // 7), M - 1])
+    for i, (y, (wq, s)) in enumerate(zip(outs, host)):
+        n = wq.shape[0]
+        cols = np.unique(np.r_[0:n:max(1, n // 300), n - 1])
+        yv = y.numpy()
+        assert yv.shape == (M, n)
+        ref = O.qmm(mode, np.ascontiguousarray(xb[rs]), wq, s, cols=cols)
+        ok, fro, worst = O.check_tolerance(O.bf16_bits_to_f32(yv[rs][:, cols]), O.bf16_bits_to_f32(ref), **TOL)
+        assert ok, (group, i, "oracle", fro, worst)
+        single = Q.quantized_matmul(x, arrs[i][0], arrs[i][1], mode).numpy()
+        ok, fro, worst = O.check_tolerance(O.bf16_bits_to_f32(yv), O.bf16_bits_to_f32(single), **TOL)
+        assert ok, (group, i, "single call", fro, worst)
+    # a second call gives the same bits (the split tiles' partials are summed in K order)
+    outs2 = Q.quantized_matmul_group(x, [a[0] for a in arrs], [a[1] for a in arrs], mode)
+    for y, y2 in zip(outs, outs2):
+        assert np.array_equal(y.numpy(), y2.numpy())
 
 
 def test_group_argument_errors():
