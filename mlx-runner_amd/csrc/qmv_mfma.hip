@@ -44,8 +44,9 @@ namespace qmm {
 namespace {
 
 constexpr int QF_REC = 272;  // x record of one (x row, 128-K chunk): 256 data bytes, then 16 zero bytes
-// x rows the record area of a wave's tile is laid out for: 4, or M when more (mxfp8, M <= 8)
-constexpr int qf_rec_rows(int M) { return M > 4 ? M : 4; }
+// x rows the record area of a wave's tile is laid out for: 4, M up to 8 (mxfp8), and 8
+// for mxfp8 x of 9-16 rows, whose records are made 8 rows at a time
+constexpr int qf_rec_rows(int M) { return M > 8 ? 8 : M > 4 ? M : 4; }
 constexpr int QF_FLUSH_MAX = 16;
 
 // Keeps a value in its own register until this point.  The scale operands of
@@ -113,9 +114,9 @@ __device__ __forceinline__ void split8(const uint4 q, uint2 &hi, uint2 &lo, int 
 //          exponent of (m, g, hi|lo, c) at 64 m + (2 g + hl) * 4 + c.
 //   mxfp8: hi at [0, 128), lo at [128, 256) in K order; exponent of
 //          (m, hi|lo, c, block) at 64 m + (4 hl + c) * 4 + block.
-template <int MODE, int M>
+template <int MODE, int M, int LR = qf_rec_rows(M)>
 __device__ __forceinline__ void qf_write_records(uint8_t *tile, const uint4 (&xin)[M], int lane) {
-  uint8_t *ex = tile + 4 * qf_rec_rows(M) * QF_REC;
+  uint8_t *ex = tile + 4 * LR * QF_REC;  // after the records of LR rows
   const int c = lane >> 4, kc = (lane & 15) * 8;  // chunk of the slice, offset in the chunk
 #pragma unroll
   for (int m = 0; m < M; ++m) {
@@ -272,41 +273,59 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
   // 3) x split into records in this wave's tile (before it holds weights), then the
   //    A operands of the slice's 4 chunks into registers, kept for the pass.
   //    E4M3 A layout: lane group h, byte t holds logical K 64 (t/16) + 16 h + t%16.
-  uint8_t *ex = tile + 4 * qf_rec_rows(M) * QF_REC;  // exponent bytes, 64 per x row
+  constexpr int LR = qf_rec_rows(M);
+  uint8_t *ex = tile + 4 * LR * QF_REC;  // exponent bytes, 64 per x row
   const int h = lane >> 4, n = lane & 15;
-  constexpr int MA = MODE == NVFP4 ? M : 1;  // A operands per chunk
+  // A operands per chunk: nvfp4 one per x row; mxfp8 one per 8 x rows (MG column groups)
+  constexpr int MG = MODE == NVFP4 ? 1 : (M + 7) / 8;
+  constexpr int MA = MODE == NVFP4 ? M : MG;
   i32x8_t areg[4][MA];
   int asreg[4][MA];
   auto prep = [&](const uint4(&xin)[M]) __attribute__((always_inline)) {
-    qf_write_records<MODE, M>(tile, xin, lane);
-    int aoff0, aoff1, am, ebase;
     if constexpr (MODE == NVFP4) {
+      qf_write_records<MODE, M>(tile, xin, lane);
       // column n = 4p + v: group g = 2p + v/2 of the chunk, hi (v even) or lo; nonzero only
       // where logical K is in group g, i.e. lane group g%4, byte half g/4
       const int pp = n >> 2, v = n & 3, g = 2 * pp + (v >> 1), hl = v & 1;
       const bool own = h == (g & 3);
-      aoff0 = own && g < 4 ? 32 * g + 16 * hl : 256;
-      aoff1 = own && g >= 4 ? 32 * g + 16 * hl : 256;
-      am = 0;
-      ebase = (g * 2 + hl) * 4;  // + m*64 + c
+      const int aoff0 = own && g < 4 ? 32 * g + 16 * hl : 256;
+      const int aoff1 = own && g >= 4 ? 32 * g + 16 * hl : 256;
+      const int ebase = (g * 2 + hl) * 4;  // + m*64 + c
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const uint8_t *rec = tile + (m * 4 + cc) * QF_REC;
+          const uint4 u0 = *(const uint4 *)(rec + aoff0), u1 = *(const uint4 *)(rec + aoff1);
+          areg[cc][m] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+          asreg[cc][m] = ex[m * 64 + ebase + cc];
+        }
     } else {
-      // column n = 2m + hl for m < M; the other columns are zero
-      const int m = n >> 1, hl = n & 1;
-      const bool lv = m < M;
-      aoff0 = lv ? 128 * hl + 16 * h : 256;
-      aoff1 = lv ? 128 * hl + 64 + 16 * h : 256;
-      am = lv ? m : 0;
-      ebase = am * 64 + hl * 16 + h;  // + 4c: block h of chunk c
+      // column group gg holds x rows 8 gg + [0, 8): column n = 2 m + hl for row 8 gg + m
+      // (the other columns are zero).  Its records are written to the tile, read into the
+      // A operands, then overwritten by the next group's (a wave's LDS accesses run in
+      // order, so the reads see this group's records).
+      auto group = [&](auto gg_c) __attribute__((always_inline)) {
+        constexpr int GG = decltype(gg_c)::value;
+        constexpr int MR = M - 8 * GG < 8 ? M - 8 * GG : 8;  // rows of this group
+        qf_write_records<MODE, MR, LR>(tile, *reinterpret_cast<const uint4(*)[MR]>(&xin[8 * GG]), lane);
+        const int m = n >> 1, hl = n & 1;
+        const bool lv = m < MR;
+        const int aoff0 = lv ? 128 * hl + 16 * h : 256;
+        const int aoff1 = lv ? 128 * hl + 64 + 16 * h : 256;
+        const int am = lv ? m : 0;
+        const int ebase = am * 64 + hl * 16 + h;  // + 4c: block h of chunk c
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          const uint8_t *rec = tile + (am * 4 + cc) * QF_REC;
+          const uint4 u0 = *(const uint4 *)(rec + aoff0), u1 = *(const uint4 *)(rec + aoff1);
+          areg[cc][GG] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+          asreg[cc][GG] = ex[ebase + 4 * cc];
+        }
+      };
+      group(std::integral_constant<int, 0>{});
+      if constexpr (MG > 1) group(std::integral_constant<int, 1>{});
     }
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-      for (int m = 0; m < MA; ++m) {
-        const uint8_t *rec = tile + ((MODE == NVFP4 ? m : am) * 4 + cc) * QF_REC;
-        const uint4 u0 = *(const uint4 *)(rec + aoff0), u1 = *(const uint4 *)(rec + aoff1);
-        areg[cc][m] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
-        asreg[cc][m] = MODE == NVFP4 ? ex[m * 64 + ebase + cc] : ex[ebase + 4 * cc];
-      }
   };
   prep(xr[0]);
 #pragma unroll
@@ -405,7 +424,9 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
           }
         }
       } else {
-        f32x4_t dd = {0.f, 0.f, 0.f, 0.f};
+        f32x4_t dd[MG];
+#pragma unroll
+        for (int gg = 0; gg < MG; ++gg) dd[gg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         int bsc[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -415,18 +436,23 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
           const uint4 b0 = *(const uint4 *)bp, b1 = *(const uint4 *)(bp + 64);
           const i32x8_t bw = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
           bsc[c] = st[n * G::SB + 4 * c + h];
-          dd = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(areg[c][0], bw, dd, 0, 0, 0, asreg[c][0], 0, bsc[c]);
-        }
-        // lane (n, h) holds columns 4h + v = (m = 2h + v/2, hi | lo)
 #pragma unroll
-        for (int v2 = 0; v2 < 2; ++v2) {
-          const int m = 2 * h + v2;
-          if (live && m < M) {
-            float *dst = pslot + (m * Q + q) * 16 + n;
-            const float a = real ? dd[2 * v2] + dd[2 * v2 + 1] : 0.f;
-            *dst = p == 0 ? a : *dst + a;
-          }
+          for (int gg = 0; gg < MG; ++gg)
+            dd[gg] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(areg[c][gg], bw, dd[gg], 0, 0, 0, asreg[c][gg], 0,
+                                                                      bsc[c]);
         }
+        // lane (n, h) holds columns 4h + v of group gg = (x row 8 gg + 2h + v/2, hi | lo)
+#pragma unroll
+        for (int gg = 0; gg < MG; ++gg)
+#pragma unroll
+          for (int v2 = 0; v2 < 2; ++v2) {
+            const int m = 8 * gg + 2 * h + v2;
+            if (live && m < M) {
+              float *dst = pslot + (m * Q + q) * 16 + n;
+              const float a = real ? dd[gg][2 * v2] + dd[gg][2 * v2 + 1] : 0.f;
+              *dst = p == 0 ? a : *dst + a;
+            }
+          }
 #pragma unroll
         for (int c = 0; c < 4; ++c) keep_live(bsc[c]);
       }
@@ -673,8 +699,9 @@ static int qf_flush_rows(const QmmArgs &a, int nrb) {
 static bool q32_ok(const QmmArgs &a);
 
 bool qmv_mfma_ok(const QmmArgs &a) {
-  // (mxfp8 holds x rows as A columns (m, hi|lo): 16 columns, up to 8 rows)
-  if (a.x_f32 || a.M < 1 || a.N < 16 || a.M > (a.mode == MXFP8 ? 8 : 4)) return false;
+  // (mxfp8 holds x rows as A columns (m, hi|lo): 16 columns per operand, 8 rows, and two
+  // operands per chunk for 9-16 rows)
+  if (a.x_f32 || a.M < 1 || a.N < 16 || a.M > (a.mode == MXFP8 ? 16 : 4)) return false;
   // nvfp4 at M = 3-4 runs the 32x32x64 form (the 16x16x128 form's A operands would
   // not fit in registers); measured faster than the unpacking GEMV from N = 4096
   // (N = 5120, K = 5120, M = 3: 7.8 against 9.4 us; gate+up M = 3: 22.8 against 30.7;
@@ -682,7 +709,8 @@ bool qmv_mfma_ok(const QmmArgs &a) {
   if (a.mode == NVFP4 && a.M > 2) return a.N >= 4096 && q32_ok(a);
   const QfShape g = qf_shape(a.K);
   if (g.Q == 0) return false;
-  if (a.M > 5 && g.P == 3) return false;  // x of three passes for 6-8 rows would not fit in registers
+  // x of every pass is held in registers: 6-8 rows fit two passes, 9-16 rows one
+  if ((a.M > 5 && g.P == 3) || (a.M > 8 && g.P > 1)) return false;
   // Where this path is faster than the unpacking GEMV (measured on the 256-CU
   // MI355X): at M = 1 only for nvfp4, with many rows per CU at K = 5120 (it pays
   // a per-workgroup x split and pipeline fill) and at K = 17408 (N = 5120: 11.8
@@ -737,11 +765,15 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
       if constexpr (M <= 5) return launch_qf<MODE, M, 12, 1, 1, 3>(a, w2, s2, grid, F, st);
       return hipErrorInvalidValue;  // (qmv_mfma_ok: x of three passes would not fit in registers)
     }
-    if (g.P == 2) return launch_qf<MODE, M, 10, 1, 1, 2>(a, w2, s2, grid, F, st);
+    if (g.P == 2) {
+      if constexpr (M <= 8) return launch_qf<MODE, M, 10, 1, 1, 2>(a, w2, s2, grid, F, st);
+      return hipErrorInvalidValue;
+    }
     if (g.Q == 12) return launch_qf<MODE, M, 12, 1, 1, 1>(a, w2, s2, grid, F, st);
   }
   // (the MLP form and the grouped form at nvfp4 M = 2 would spill with two units in flight)
-  if constexpr (!((NMAT == 2 || PARTS) && MODE == NVFP4 && M == 2))
+  // (nor x of 9-16 rows, whose x and A operands take twice the registers)
+  if constexpr (!((NMAT == 2 || PARTS) && MODE == NVFP4 && M == 2) && M <= 8)
     if (nrb <= 4) return launch_qf<MODE, M, 10, NMAT, 2, 1, PARTS>(a, w2, s2, grid, F, st);
   return launch_qf<MODE, M, 10, NMAT, 1, 1, PARTS>(a, w2, s2, grid, F, st);
 }
@@ -765,6 +797,14 @@ static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8
       case 6: return launch_qf_d<MXFP8, 6, 1>(a, w2, s2, grid, F, nrb, st);
       case 7: return launch_qf_d<MXFP8, 7, 1>(a, w2, s2, grid, F, nrb, st);
       case 8: return launch_qf_d<MXFP8, 8, 1>(a, w2, s2, grid, F, nrb, st);
+      case 9: return launch_qf_d<MXFP8, 9, 1>(a, w2, s2, grid, F, nrb, st);
+      case 10: return launch_qf_d<MXFP8, 10, 1>(a, w2, s2, grid, F, nrb, st);
+      case 11: return launch_qf_d<MXFP8, 11, 1>(a, w2, s2, grid, F, nrb, st);
+      case 12: return launch_qf_d<MXFP8, 12, 1>(a, w2, s2, grid, F, nrb, st);
+      case 13: return launch_qf_d<MXFP8, 13, 1>(a, w2, s2, grid, F, nrb, st);
+      case 14: return launch_qf_d<MXFP8, 14, 1>(a, w2, s2, grid, F, nrb, st);
+      case 15: return launch_qf_d<MXFP8, 15, 1>(a, w2, s2, grid, F, nrb, st);
+      case 16: return launch_qf_d<MXFP8, 16, 1>(a, w2, s2, grid, F, nrb, st);
       default: break;
     }
   }

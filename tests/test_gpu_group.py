@@ -158,12 +158,12 @@ def test_group_prefill_one_gemm(mode):
     check_parts(mode, xb, outs, host, "prefill")
 
 
-# The model's groups at prefill sizes: M = 16 and 96 run split tiles (each tile's K over
+# The model's groups at prefill sizes: M = 24 and 96 run split tiles (each tile's K over
 # several blocks, then the reduce stores to the parts), M = 300 whole tiles with a partial
 # last round (mxfp8: 128-tiles in the same launch; nvfp4: 128-row tiles).  Parts whose
 # rows are not a multiple of 8 (ragged) take element stores throughout.
 @pytest.mark.parametrize("mode", ["nvfp4", "mxfp8"])
-@pytest.mark.parametrize("group,M", [("gdn_in_proj", 16), ("gdn_in_proj", 300), ("attn_qkv", 96),
+@pytest.mark.parametrize("group,M", [("gdn_in_proj", 24), ("gdn_in_proj", 300), ("attn_qkv", 96),
                                      ("attn_qkv", 300), ("ragged_small", 64), ("ragged_big", 200)])
 def test_group_prefill_model_shapes(mode, group, M):
     rows, K = GROUPS[group], 5120
