@@ -583,7 +583,7 @@ __global__ __launch_bounds__(F_THREADS, 2) void gemm_mxfp8_pipe_ksplit128_kernel
     const YOut yo, int M, int N, int K, int S, float *__restrict__ part) {
   const int b = blockIdx.x, t = b / S, k = b - t * S, steps = K / P_BK;
   pipe_tile<128>(t, xh, xl, sh, sl, w, sw, yo, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S,
-                 part + (size_t)b * 128 * 128);
+                 part ? part + (size_t)b * 128 * 128 : nullptr);
 }
 
 // The split tiles' results (TS-tiles of W rows [n_split, N)): one thread per float4 of a
@@ -648,8 +648,9 @@ bool gemm_mxfp8_ok(const QmmArgs &a) {
 //   * else the last round runs as it falls (n_split = N).
 // (Split tiles for a last partial round of a larger call measured slower at M = 4096,
 // N = 17408, K = 5120: the 64 MiB of partial sums cost more than the 128-tiles lose.)
-// x of at most 128 rows with at most one 128-tile per CU splits 128-tiles instead, two
-// blocks per CU (TS = 128).
+// x of at most 128 rows runs 128-tiles instead, two blocks per CU (TS = 128): split S
+// ways along K where they leave block slots idle, whole (S = 1, stored directly) where
+// there are more of them than slots.
 struct Fp8Plan {
   int n_split, tiles1, tail_tiles, S, TS;
 };
@@ -665,9 +666,9 @@ static Fp8Plan fp8_plan(const QmmArgs &a, int cus) {
   Fp8Plan p{a.N, T, 0, 0, 256};
   if (cus <= 0) return p;
   const int T128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
-  if (a.M <= 128 && T128 <= cus) {
+  if (a.M <= 128) {
     const int S = fp8_split_ways(T128, 2 * cus, steps);
-    if (S) return Fp8Plan{0, 0, T128, S, 128};
+    return Fp8Plan{0, 0, T128, S ? S : 1, 128};
   }
   if (2 * T <= cus) {
     const int S = fp8_split_ways(T, cus, steps);
@@ -767,9 +768,10 @@ hipError_t launch_gemm_mxfp8(const QmmArgs &a, void *ws, hipStream_t st) {
       e = ensure_dynamic_lds(lds128, (const void *)gemm_mxfp8_pipe_ksplit128_kernel, (int)PipeGeom<128>::LDS);
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(gemm_mxfp8_pipe_ksplit128_kernel, dim3(p.tail_tiles * p.S), dim3(F_THREADS),
-                         PipeGeom<128>::LDS, st, xh, xl, sh, sl, a.w, swp, yo, a.M, a.N, a.K, p.S, part);
+                         PipeGeom<128>::LDS, st, xh, xl, sh, sl, a.w, swp, yo, a.M, a.N, a.K, p.S,
+                         p.S >= 2 ? part : (float *)nullptr);
       e = hipGetLastError();
-      if (e != hipSuccess) return e;
+      if (e != hipSuccess || p.S < 2) return e;
       hipLaunchKernelGGL(gemm_mxfp8_split_reduce_kernel<128>, dim3(p.tail_tiles * fp8_reduce_blocks<128>()), dim3(256), 0,
                          st, (const float *)part, yo, a.M, a.N, 0, p.S);
       return hipGetLastError();

@@ -291,7 +291,8 @@ __device__ __forceinline__ void nv_ksplit_block(const uint16_t *__restrict__ x, 
                                                 const uint8_t *__restrict__ sp, const YOut yo, int M,
                                                 int N, int K, int S, float *__restrict__ part) {
   const int b = blockIdx.x, t = b / S, k = b - t * S, steps = K / V_BK;
-  nv_tile<TM>(t, x, w, sp, yo, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S, part + (size_t)b * TM * 256);
+  nv_tile<TM>(t, x, w, sp, yo, M, N, K, 0, N, k * steps / S, (k + 1) * steps / S,
+              part ? part + (size_t)b * TM * 256 : nullptr);
 }
 template <int TM>
 __global__ __launch_bounds__(V_THREADS) void gemm_nvfp4_pipe_ksplit_kernel(const uint16_t *__restrict__ x,
@@ -359,21 +360,24 @@ bool gemm_nvfp4_ok(const QmmArgs &a) {
          (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.w % 16 == 0 && (uintptr_t)a.s % 4 == 0;
 }
 
-// A call of at most half as many tiles as CUs runs every tile split S ways along K (at
-// most one round of blocks, each at least 8 K steps), with 64-row tiles (two blocks per
-// CU) when x has at most 64 rows and 128-row tiles up to 128 rows: the split plan, or
-// S = 0 for the whole-tile paths.
+// x of at most 128 rows runs its own tile height, 64 rows (two blocks per CU) up to 64
+// rows and 128 up to 128, split S ways along K where the tiles leave block slots idle (at
+// most one round of blocks, each at least 8 K steps) and whole (S = 1, stored directly)
+// where there are more tiles than slots.  Taller x runs 256-row tiles, split the same way
+// when a call has at most half as many tiles as CUs: the plan, or S = 0 for the
+// whole-tile paths.
 struct NvSplit {
   int TM, tiles, S;
 };
 static NvSplit nv_split_plan(const QmmArgs &a, int cus) {
   const int TM = a.M <= 64 ? 64 : a.M <= 128 ? 128 : 256;
   const int T = ((a.M + TM - 1) / TM) * ((a.N + V_BN - 1) / V_BN), steps = a.K / V_BK;
-  if (cus <= 0 || 2 * T > cus) return NvSplit{TM, T, 0};
+  if (cus <= 0 || (TM == 256 && 2 * T > cus)) return NvSplit{TM, T, 0};
   int S = (TM == 64 ? 2 * cus : cus) / T;
   if (S > 8) S = 8;
   if (S > steps / 8) S = steps / 8;
-  return NvSplit{TM, T, S >= 2 ? S : 0};
+  if (S >= 2) return NvSplit{TM, T, S};
+  return NvSplit{TM, T, TM == 256 ? 0 : 1};
 }
 
 // Workspace: the scales repacked tile-major, unless they come so (a.s_tiled), then (split
@@ -381,7 +385,7 @@ static NvSplit nv_split_plan(const QmmArgs &a, int cus) {
 size_t gemm_nvfp4_workspace(const QmmArgs &a) {
   size_t bytes = a.s_tiled ? 0 : round256v(a.N) * (size_t)(a.K / 16);
   const NvSplit p = nv_split_plan(a, device_cu_count());
-  if (p.S) bytes = round256v(bytes) + (size_t)p.tiles * p.S * p.TM * 256 * 4;
+  if (p.S >= 2) bytes = round256v(bytes) + (size_t)p.tiles * p.S * p.TM * 256 * 4;
   return bytes + 256;
 }
 
@@ -405,27 +409,29 @@ hipError_t launch_gemm_nvfp4(const QmmArgs &a, void *ws, hipStream_t st) {
   const YOut yo = yout_of(a);  // y, or a grouped call's parts
   const NvSplit sp = nv_split_plan(a, device_cu_count());
   if (sp.S) {
-    float *part = (float *)((uint8_t *)ws + round256v(a.s_tiled ? 0 : round256v(a.N) * (size_t)(a.K / 16)));
+    // (S = 1: whole tiles of this height, stored directly: no partial sums, no reduce)
+    float *part = sp.S >= 2 ? (float *)((uint8_t *)ws + round256v(a.s_tiled ? 0 : round256v(a.N) * (size_t)(a.K / 16)))
+                            : nullptr;
     const int blocks = sp.tiles * sp.S;
     if (sp.TM == 64) {
       hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit64_kernel, dim3(blocks), dim3(V_THREADS), NvGeom<64>::LDS, st,
                          (const uint16_t *)a.x, a.w, tiled, yo, a.M, a.N, a.K, sp.S, part);
       e = hipGetLastError();
-      if (e == hipSuccess)
+      if (e == hipSuccess && part)
         hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<64>, dim3(sp.tiles * nv_reduce_blocks<64>()), dim3(256), 0,
                            st, (const float *)part, yo, a.M, a.N, sp.S);
     } else if (sp.TM == 128) {
       hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit_kernel<128>, dim3(blocks), dim3(V_THREADS), V_LDS, st,
                          (const uint16_t *)a.x, a.w, tiled, yo, a.M, a.N, a.K, sp.S, part);
       e = hipGetLastError();
-      if (e == hipSuccess)
+      if (e == hipSuccess && part)
         hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<128>, dim3(sp.tiles * nv_reduce_blocks<128>()), dim3(256), 0,
                            st, (const float *)part, yo, a.M, a.N, sp.S);
     } else {
       hipLaunchKernelGGL(gemm_nvfp4_pipe_ksplit_kernel<256>, dim3(blocks), dim3(V_THREADS), V_LDS, st,
                          (const uint16_t *)a.x, a.w, tiled, yo, a.M, a.N, a.K, sp.S, part);
       e = hipGetLastError();
-      if (e == hipSuccess)
+      if (e == hipSuccess && part)
         hipLaunchKernelGGL(gemm_nvfp4_split_reduce_kernel<256>, dim3(sp.tiles * nv_reduce_blocks<256>()), dim3(256), 0,
                            st, (const float *)part, yo, a.M, a.N, sp.S);
     }

@@ -542,26 +542,37 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
   };
   load_unit(0, 0);
 
-  // A operands of the slice's 8 chunks (see above), from the x records
+  // A operands of the slice's 8 chunks (see above), from the x records; x of 5-8 rows
+  // takes two operands per chunk, operand G holding rows 4 G + [0, 4)
+  constexpr int MG = (M + 3) / 4;
   const int i = lane & 31, h = lane >> 5;
   const int am = i >> 3, ag = (i >> 1) & 3, ahl = i & 1;
-  const bool alive = am < M, own0 = alive && ag == h, own1 = alive && ag == 2 + h;
   // A lane (i, h) is nonzero in bytes 0-15 (own0) or 16-31 (own1) or nowhere, the
   // same half for every chunk: only those 16 bytes are kept, the operand is
   // rebuilt with masks at each MFMA
-  const uint32_t amask0 = own0 ? 0xFFFFFFFFu : 0u, amask1 = own1 ? 0xFFFFFFFFu : 0u;
+  uint32_t amask0[MG], amask1[MG];
+  int arec[MG], aex[MG];
   const int aoff = 32 * ag + 16 * ahl;  // in record (m, c8 / 2), + 128 for odd c8
-  const int arec = (alive ? am : 0) * 4, aex = 4 * 4 * QF_REC + (alive ? am : 0) * 64 + (ag * 2 + ahl) * 4;
-  uint4 areg[8];
-  int asreg[8];
+#pragma unroll
+  for (int G = 0; G < MG; ++G) {
+    const bool alive = 4 * G + am < M;
+    amask0[G] = alive && ag == h ? 0xFFFFFFFFu : 0u;
+    amask1[G] = alive && ag == 2 + h ? 0xFFFFFFFFu : 0u;
+    arec[G] = (alive ? 4 * G + am : 0) * 4;
+    aex[G] = 4 * qf_rec_rows(M) * QF_REC + (alive ? 4 * G + am : 0) * 64 + (ag * 2 + ahl) * 4;
+  }
+  uint4 areg[8][MG];
+  int asreg[8][MG];
   auto prep = [&]() __attribute__((always_inline)) {
     qf_write_records<NVFP4, M>(tile, xr, lane);
 #pragma unroll
-    for (int c8 = 0; c8 < 8; ++c8) {
-      // 64-element chunk c8 = half c8 % 2 of 128-element record c8 / 2: groups 4 (c8 % 2) + [0, 4)
-      areg[c8] = *(const uint4 *)(tile + (arec + (c8 >> 1)) * QF_REC + 128 * (c8 & 1) + aoff);
-      asreg[c8] = tile[aex + 4 * 8 * (c8 & 1) + (c8 >> 1)];
-    }
+    for (int c8 = 0; c8 < 8; ++c8)
+#pragma unroll
+      for (int G = 0; G < MG; ++G) {
+        // 64-element chunk c8 = half c8 % 2 of 128-element record c8 / 2: groups 4 (c8 % 2) + [0, 4)
+        areg[c8][G] = *(const uint4 *)(tile + (arec[G] + (c8 >> 1)) * QF_REC + 128 * (c8 & 1) + aoff);
+        asreg[c8][G] = tile[aex[G] + 4 * 8 * (c8 & 1) + (c8 >> 1)];
+      }
   };
 
   auto flush = [&](int rb_first, int rb_last) __attribute__((always_inline)) {
@@ -625,19 +636,30 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
         for (int m = 0; m < M; ++m) asm volatile("" : "+v"(b0) : "v"(acc[m]));
         const i32x8_t bw = {b0, (int)b.y, (int)b.z, (int)b.w, 0, 0, 0, 0};
         const f32x2_t sc = __builtin_amdgcn_cvt_pk_f32_fp8((int)*(const uint16_t *)(st + i * 32 + 4 * c8 + 2 * h), false);
-        // (the masks pass through asm so that the masked operands are not hoisted out of
-        // the loop as invariants: that would hold all 8 full operands in registers)
-        uint32_t k0 = amask0, k1 = amask1;
-        asm volatile("" : "+v"(k0), "+v"(k1));
-        const uint4 ad = areg[c8];
-        const i32x8_t aw = {(int)(ad.x & k0), (int)(ad.y & k0), (int)(ad.z & k0), (int)(ad.w & k0),
-                            (int)(ad.x & k1), (int)(ad.y & k1), (int)(ad.z & k1), (int)(ad.w & k1)};
-        const f32x16_t dd = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-            aw, bw, f32x16_t{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, 0, 4,
-            0, asreg[c8], 0, 127);
 #pragma unroll
-        for (int m = 0; m < M; ++m)
-          acc[m] += sc.x * (dd[4 * m] + dd[4 * m + 1]) + sc.y * (dd[4 * m + 2] + dd[4 * m + 3]);
+        for (int G = 0; G < MG; ++G) {
+          // (the masks pass through asm so that the masked operands are not hoisted out of
+          // the loop as invariants: that would hold all 8 full operands in registers)
+          uint32_t k0 = amask0[G], k1 = amask1[G];
+          asm volatile("" : "+v"(k0), "+v"(k1));
+          const uint4 ad = areg[c8][G];
+          const i32x8_t aw = {(int)(ad.x & k0), (int)(ad.y & k0), (int)(ad.z & k0), (int)(ad.w & k0),
+                              (int)(ad.x & k1), (int)(ad.y & k1), (int)(ad.z & k1), (int)(ad.w & k1)};
+          int bg0 = bw[0];
+          if constexpr (MG > 1) {  // operand G's MFMA after operand G - 1's sums (one output live)
+#pragma unroll
+            for (int m = 0; m < M; ++m) asm volatile("" : "+v"(bg0) : "v"(acc[m]));
+          }
+          const i32x8_t bwg = {bg0, bw[1], bw[2], bw[3], 0, 0, 0, 0};
+          const f32x16_t dd = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+              aw, bwg, f32x16_t{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, 0, 4,
+              0, asreg[c8][G], 0, 127);
+#pragma unroll
+          for (int mm = 0; mm < 4; ++mm) {
+            const int m = 4 * G + mm;
+            if (m < M) acc[m] += sc.x * (dd[4 * mm] + dd[4 * mm + 1]) + sc.y * (dd[4 * mm + 2] + dd[4 * mm + 3]);
+          }
+        }
       }
       // every lane stores its half's sums (no branch: the compiler would sink the
       // accumulation of rows m > 0 into it and keep all chunks' outputs live)
@@ -648,7 +670,9 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
         *dst = p == 0 ? a : *dst + a;
       }
 #pragma unroll
-      for (int c8 = 0; c8 < 8; ++c8) keep_live(asreg[c8]);
+      for (int c8 = 0; c8 < 8; ++c8)
+#pragma unroll
+        for (int G = 0; G < MG; ++G) keep_live(asreg[c8][G]);
       // with several passes the host sets F >= nrb: one flush, after the last pass
       if (p == P - 1 && (rbf + 1 == F || rb + 1 == nrb)) flush(rb - rbf, rb);
       rbf = rbf + 1 == F ? 0 : rbf + 1;
@@ -700,8 +724,9 @@ static bool q32_ok(const QmmArgs &a);
 
 bool qmv_mfma_ok(const QmmArgs &a) {
   // (mxfp8 holds x rows as A columns (m, hi|lo): 16 columns per operand, 8 rows, and two
-  // operands per chunk for 9-16 rows)
-  if (a.x_f32 || a.M < 1 || a.N < 16 || a.M > (a.mode == MXFP8 ? 16 : 4)) return false;
+  // operands per chunk for 9-16 rows; nvfp4 runs 3-8 rows on the 32x32x64 form, two
+  // operands per chunk from 5 rows)
+  if (a.x_f32 || a.M < 1 || a.N < 16 || a.M > (a.mode == MXFP8 ? 16 : 8)) return false;
   // nvfp4 at M = 3-4 runs the 32x32x64 form (the 16x16x128 form's A operands would
   // not fit in registers); measured faster than the unpacking GEMV from N = 4096
   // (N = 5120, K = 5120, M = 3: 7.8 against 9.4 us; gate+up M = 3: 22.8 against 30.7;
@@ -844,9 +869,10 @@ static int q32_flush_rows(const QmmArgs &a, int nrb) {
 }
 
 static bool q32_ok(const QmmArgs &a) {
-  if (a.mode != NVFP4 || a.x_f32 || a.M < 1 || a.M > 4 || a.N < 16) return false;
+  if (a.mode != NVFP4 || a.x_f32 || a.M < 1 || a.M > 8 || a.N < 16) return false;
   const QfShape g = qf_shape(a.K);
   if (g.Q == 0 || qf_cus() == 0) return false;
+  if (a.M > 4 && g.P > 1) return false;  // x of 5-8 rows: one pass (two A operands per chunk)
   if (g.P > 1 && q32_flush_rows(a, q32_nrb(a, qf_cus())) < q32_nrb(a, qf_cus())) return false;
   if ((int64_t)a.N * (a.K / 2) >= ((int64_t)1 << 32)) return false;  // 32-bit offsets within W
   return ((((uintptr_t)a.x) | ((uintptr_t)a.w) | ((uintptr_t)a.s)) & 15) == 0;
@@ -855,8 +881,12 @@ static bool q32_ok(const QmmArgs &a) {
 // the plain 32-row form for K's (Q, P)
 template <int M>
 static hipError_t launch_q32_k(const QmmArgs &a, QfShape g, int grid, int F, hipStream_t st) {
-  if (g.P == 3) return launch_q32<M, 12, 3, 1>(a, a.w, a.s, grid, F, st);
-  if (g.P == 2) return launch_q32<M, 10, 2, 1>(a, a.w, a.s, grid, F, st);
+  if constexpr (M <= 4) {
+    if (g.P == 3) return launch_q32<M, 12, 3, 1>(a, a.w, a.s, grid, F, st);
+    if (g.P == 2) return launch_q32<M, 10, 2, 1>(a, a.w, a.s, grid, F, st);
+  } else if (g.P > 1) {
+    return hipErrorInvalidValue;
+  }
   if (g.Q == 12) return launch_q32<M, 12, 1, 1>(a, a.w, a.s, grid, F, st);
   return launch_q32<M, 10, 1, 1>(a, a.w, a.s, grid, F, st);
 }
@@ -871,7 +901,7 @@ static hipError_t launch_q32_any(const QmmArgs &a, hipStream_t st) {
   const QfShape g = qf_shape(a.K);
   const uint8_t *w2 = a.w, *s2 = a.s;  // unused in the plain form
   if (a.parts) {  // grouped calls: K = 5120, M = 3-4
-    if (g.Q != 10 || g.P != 1 || a.M < 3) return hipErrorInvalidValue;
+    if (g.Q != 10 || g.P != 1 || a.M < 3 || a.M > 4) return hipErrorInvalidValue;
     return a.M == 3 ? launch_q32<3, 10, 1, 1, true>(a, w2, s2, grid, F, st)
                     : launch_q32<4, 10, 1, 1, true>(a, w2, s2, grid, F, st);
   }
@@ -879,13 +909,17 @@ static hipError_t launch_q32_any(const QmmArgs &a, hipStream_t st) {
     case 1: return launch_q32_k<1>(a, g, grid, F, st);
     case 2: return launch_q32_k<2>(a, g, grid, F, st);
     case 3: return launch_q32_k<3>(a, g, grid, F, st);
-    default: return launch_q32_k<4>(a, g, grid, F, st);
+    case 4: return launch_q32_k<4>(a, g, grid, F, st);
+    case 5: return launch_q32_k<5>(a, g, grid, F, st);
+    case 6: return launch_q32_k<6>(a, g, grid, F, st);
+    case 7: return launch_q32_k<7>(a, g, grid, F, st);
+    default: return launch_q32_k<8>(a, g, grid, F, st);
   }
 }
 
 // The MLP form at nvfp4 M = 3-4 (K = 5120, one pass).
 static bool q32_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up) {
-  return a.M >= 3 && q32_ok(a) && qf_shape(a.K).P == 1 && ((((uintptr_t)w_up) | ((uintptr_t)s_up)) & 15) == 0;
+  return a.M >= 3 && a.M <= 4 && q32_ok(a) && qf_shape(a.K).P == 1 && ((((uintptr_t)w_up) | ((uintptr_t)s_up)) & 15) == 0;
 }
 
 static hipError_t launch_q32_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st) {

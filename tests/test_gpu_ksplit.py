@@ -30,12 +30,17 @@ def _case(mode, M, N, K, seed):
     return x, wq, sc
 
 
-# (mode, M, N, K): 128-row tiles (nvfp4, M <= 128) and 256-row tiles, one to 68 tile columns
+# (mode, M, N, K): 128-row tiles (nvfp4, M <= 128) and 256-row tiles, one to 68 tile columns;
+# then x of at most 128 rows with more tiles than block slots (whole tiles of the short
+# height, stored without partial sums) or between half and all of them (nvfp4 M = 9 at the
+# fused gate+up width: 136 tiles of 64 rows, split 3 ways)
 SHAPES = [
     ("nvfp4", 16, 17408, 5120), ("nvfp4", 100, 5120, 5120), ("nvfp4", 128, 12288, 5120),
     ("nvfp4", 129, 4096, 5120), ("nvfp4", 256, 17408, 5120), ("nvfp4", 40, 1000, 1024),
     ("mxfp8", 16, 17408, 5120), ("mxfp8", 64, 5120, 6144), ("mxfp8", 256, 17408, 5120),
     ("mxfp8", 300, 1000, 1024), ("mxfp8", 9, 2048, 10240),
+    ("nvfp4", 9, 34816, 5120), ("nvfp4", 16, 70001, 1024), ("nvfp4", 100, 40000, 1024),
+    ("mxfp8", 20, 40000, 1024), ("mxfp8", 128, 34816, 1024),
 ]
 
 

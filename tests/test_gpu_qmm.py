@@ -379,14 +379,15 @@ def make_x(rng, M, K, kind):
 # nvfp4 M = 3-4 runs the 32x32x64 form (32-row blocks, flushes every 4 blocks);
 # mxfp8 M = 5-8 the 16x16x128 form with all 16 A columns (8 rows x hi|lo) live, M = 9-16
 # with two A operands per chunk (their records made 8 rows at a time); nvfp4 M = 5-8 the
-# prefill GEMM's split tiles.
+# 32x32x64 form with two A operands per chunk (rows 4 G + [0, 4) in operand G).
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 1, 70001), ("nvfp4", 2, 4099),
                                       ("nvfp4", 2, 16384), ("nvfp4", 3, 4099), ("nvfp4", 3, 70001),
                                       ("nvfp4", 4, 16400), ("mxfp8", 2, 4101), ("mxfp8", 3, 8192),
                                       ("mxfp8", 4, 4096), ("mxfp8", 4, 70001), ("mxfp8", 5, 4101),
                                       ("mxfp8", 6, 8192), ("mxfp8", 7, 4096), ("mxfp8", 8, 70001),
                                       ("mxfp8", 9, 4101), ("mxfp8", 12, 8192), ("mxfp8", 15, 4096),
-                                      ("mxfp8", 16, 70001), ("nvfp4", 5, 4099), ("nvfp4", 8, 16400)])
+                                      ("mxfp8", 16, 70001), ("nvfp4", 5, 4099), ("nvfp4", 6, 70001),
+                                      ("nvfp4", 7, 5120), ("nvfp4", 8, 16400)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
 def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
     K = 5120
