@@ -109,11 +109,13 @@ int qmm_quantized_matmul(qmm_array *res, qmm_array x, qmm_array w, qmm_array sca
  * qlinear calls on one x: the GDN layer's in_proj_qkv / z / b / a
  * (src/model.zig:1066-1074) and attention's q / k / v (:929-944).  When the
  * matrices lie back to back in memory, and so do their scales (in any order;
- * qmm_weights_load places each layer's groups so), and M <= 4 with bfloat16 x,
- * one kernel runs over them as one matrix; otherwise one call per matrix.  Either
- * way res[i] meets the bar of qmm_quantized_matmul(x, w[i], scales[i]); the one
- * launch picks its kernel by the total row count, which can differ from the
- * single call's choice, so the bf16 roundings of the two may differ. */
+ * qmm_weights_load places each layer's groups so), with bfloat16 x, one kernel
+ * runs over them as one matrix: the decode kernel at M <= 4, the prefill GEMM at
+ * the sizes it takes (the stacked scales are then repacked per call); otherwise one
+ * call per matrix.  Either way res[i] meets the bar of
+ * qmm_quantized_matmul(x, w[i], scales[i]); the one launch picks its kernel and tiling
+ * by the total row count, which can differ from the single call's choice, so the bf16
+ * roundings of the two may differ. */
 int qmm_quantized_matmul_group(qmm_array *res, size_t n, qmm_array x, const qmm_array *w, const qmm_array *scales,
                                qmm_optional_int group_size, qmm_optional_int bits, const char *mode,
                                qmm_stream s);
