@@ -234,6 +234,8 @@ def queued_timed(step, steps, reps=5):
 
     import qmm as Q
 
+    if not hasattr(torch.cuda, "_sleep"):  # (torch's spin kernel; absent: time a graph replay)
+        return None
     st = Q.Stream.torch_current()
     t0, launches, host = time.perf_counter(), 0, []
     while True:  # untimed batches until the clocks hold: at least 1 s and 2000 launches (at most 3 s)
