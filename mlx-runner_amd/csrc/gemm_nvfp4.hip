@@ -111,50 +111,52 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   // rows 8 g + [0, 8) of the tile.  When all 8 are past the last x row (a short x), it moves
   // 4 bytes per lane instead of 16: the same instruction count (the waits count them), a
   // quarter of the bytes, and those rows' results are not stored.
-  const uint8_t *ga[XD];
+  // Every DMA source is a wave-uniform base (SGPRs: the tile's first row and the step)
+  // plus a 32-bit lane offset within the tile's rows.
+  const uint8_t *xb = (const uint8_t *)x + (int64_t)m0 * K * 2;
+  uint32_t xoff[XD];
   bool xdead[XD];
 #pragma unroll
   for (int i = 0; i < XD; ++i) {
     const int g = wave + 8 * i;
     const int q = 64 * g + lane, row = q >> 3, part = (q & 7) ^ aswz(row);
-    ga[i] = (const uint8_t *)x + ((int64_t)min(m0 + row, M - 1) * K + part * 8) * 2;
+    xoff[i] = (uint32_t)((min(m0 + row, M - 1) - m0) * K + part * 8) * 2;
     xdead[i] = m0 + 8 * g >= M;
   }
   // W: wave w moves rows 32 w + lane / 2, LDS half lane % 2 of the row (the row's half
   // (lane % 2) ^ wswz(row) of the step's 32 bytes)
   const int wr = 32 * wave + (lane >> 1);
-  const uint8_t *gw = w + (int64_t)min(n0 + wr, N - 1) * wrow + 16 * ((lane & 1) ^ wswz(wr));
+  const uint8_t *wb = w + (int64_t)n0 * wrow;
+  const uint32_t woff = (uint32_t)((min(n0 + wr, N - 1) - n0) * wrow) + 16 * ((lane & 1) ^ wswz(wr));
   // scales: wave 0, lane l copies the scale dwords of rows 4 l .. 4 l + 3 (the step's 1 KiB block)
-  const uint8_t *gs = sp + ((int64_t)(n0 >> 8) * steps * 256 + 4 * lane) * 4;
+  const uint8_t *sb = sp + (int64_t)(n0 >> 8) * steps * 1024;
+  const uint32_t soff = 16 * lane;
   const bool sw = wave == 0;
   auto issue = [&](int s) __attribute__((always_inline)) {
     const uint32_t st = lds0 + (uint32_t)((s % V_STAGES) * G::STAGE);
 #pragma unroll
     for (int i = 0; i < XD; ++i) {
-      if (xdead[i]) gp_dma4(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
-      else gp_dma16(ga[i] + s * 128, st + (wave + 8 * i) * 1024);
+      if (xdead[i]) gp_dma4s(xb + s * 128, xoff[i], st + (wave + 8 * i) * 1024);
+      else gp_dma16s(xb + s * 128, xoff[i], st + (wave + 8 * i) * 1024);
     }
-    gp_dma16(gw + s * 32, st + G::ATILE + wave * 1024);
-    if (sw) gp_dma16(gs + s * 1024, st + G::ATILE + V_WTILE);
+    gp_dma16s(wb + s * 32, woff, st + G::ATILE + wave * 1024);
+    if (sw) gp_dma16s(sb + s * 1024, soff, st + G::ATILE + V_WTILE);
   };
 
   // fragment geometry (32x32x16 bf16 operands: lane l holds row l % 32 and, in
   // sub-step ks, the step's elements 32 fh + 8 ks + [0, 8) with fh = l / 32:
   // x slot 4 fh + ks, W dword 4 fh + ks)
   const int fr = lane & 31, fh = lane >> 5;
-  int oa[FI], ab[FI], ob[FJ], os[FJ];
+  // (32 rows apart, fragments differ by whole 16-row swizzle periods, so one lane offset
+  // per sub-step serves every fragment: x fragment i of sub-step ks at xo[ks] + 4096 i, W
+  // fragment j at ob + 1024 j, its scale dword at os + 128 j)
+  const int ra = wm * WM + fr, rb = wn * WN + fr;
+  const int ab = (4 * fh) ^ aswz(ra);  // physical slot of logical slot 4 fh + ks is ks ^ ab
+  int xo[4];
 #pragma unroll
-  for (int i = 0; i < FI; ++i) {
-    const int r = wm * WM + i * 32 + fr;
-    oa[i] = r * 128;
-    ab[i] = (4 * fh) ^ aswz(r);  // physical slot of logical slot 4 fh + ks is ks ^ ab
-  }
-#pragma unroll
-  for (int j = 0; j < FJ; ++j) {
-    const int r = wn * WN + j * 32 + fr;
-    ob[j] = G::ATILE + r * 32 + 16 * (fh ^ wswz(r));
-    os[j] = G::ATILE + V_WTILE + r * 4;
-  }
+  for (int ks = 0; ks < 4; ++ks) xo[ks] = ra * 128 + 16 * (ks ^ ab);
+  const int ob = G::ATILE + rb * 32 + 16 * (fh ^ wswz(rb));
+  const int os = G::ATILE + V_WTILE + rb * 4;
 
   f32x16_t acc[FI][FJ];
 #pragma unroll
@@ -164,14 +166,22 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  // Ping-pong (as in the mxfp8 kernel): group 0 (waves 0-3) loads step k's W
-  // fragments in interval 2k and computes in 2k + 1, group 1 (waves 4-7) one
-  // interval later; each SIMD holds one wave of each group.  Stage k is read up
-  // to interval 2k + 2 (group 1's computing interval reads x), so DMA(k + 2),
-  // which refills stage k - 1, is issued by both groups in interval 2k + 1
-  // (group 0 at the start of its computing interval, group 1 in its loading
-  // interval); at the barrier ending interval 2k + 1 every wave waits for its
-  // DMA(k + 1) (only DMA(k + 2), DMA_S / DMA loads, may remain in flight).
+  // Ping-pong (as in the mxfp8 kernel): group 0 (waves 0-3) loads step k in interval 2k
+  // and computes it in 2k + 1, group 1 (waves 4-7) one interval later; each SIMD holds one
+  // wave of each group.
+  //   * Loading interval: every LDS read of the step (the W fragments and scales, and the
+  //     x fragments of all four sub-steps), then the DMAs of step k + 2, then the
+  //     dequantization of sub-step 0.  Stage k is therefore last read in interval 2k + 1,
+  //     and DMA(k + 2), which refills stage k - 1, can be issued by each group in its
+  //     loading interval of step k (2k, 2k + 1); at the barrier ending interval 2k + 1
+  //     every wave waits for its DMA(k + 1) (only DMA(k + 2), DMA_S / DMA loads, remain).
+  //   * Computing interval: the 32 MFMAs (8 per sub-step), with the dequantization of
+  //     sub-steps 1-3 interleaved, four VALU instructions after each MFMA.  The VALU work
+  //     runs beside the wave's own MFMAs, and both intervals of a SIMD carry some of it.
+  //     (Measured at lm_head prefill against other splits: all four sub-steps dequantized
+  //     in the loading interval 4.3% slower, two of them 1-2% slower; 3 or 2 VALU per
+  //     MFMA 5-8% slower; the DMAs issued before the LDS reads within 1%, after the
+  //     dequantization 5% slower.)
   const int grp = wave >> 2;
   issue(s_begin);
   if (s_end - s_begin > 1) issue(s_begin + 1);
@@ -182,60 +192,61 @@ __device__ __forceinline__ void nv_tile(int bid, const uint16_t *__restrict__ x,
   auto pp_step = [&](auto grp_c, auto dma_c, int s) __attribute__((always_inline)) {
     constexpr int GRP = decltype(grp_c)::value;
     constexpr bool DMA = decltype(dma_c)::value;
-    if constexpr (DMA && GRP == 1) issue(s + 2);  // interval 2s + 1
     const uint8_t *st = lds + (s % V_STAGES) * G::STAGE;
     uint4 wq[FJ];
     uint32_t wsc[FJ];
 #pragma unroll
     for (int j = 0; j < FJ; ++j) {
-      wq[j] = *(const uint4 *)(st + ob[j]);
-      wsc[j] = *(const uint32_t *)(st + os[j]);
+      wq[j] = *(const uint4 *)(st + ob + 1024 * j);
+      wsc[j] = *(const uint32_t *)(st + os + 128 * j);
     }
-    // W is dequantized here, in the loading interval, so that this VALU work runs
-    // beside the other group's MFMAs and the computing interval is MFMAs only
-    bf16x8_t bf[4][FJ];
+    bf16x8_t af[4][FI];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int j = 0; j < FJ; ++j) {
-        const uint32_t word = ks == 0 ? wq[j].x : ks == 1 ? wq[j].y : ks == 2 ? wq[j].z : wq[j].w;
-        bf[ks][j] = deq8_nvfp4(word, (wsc[j] >> (8 * (2 * fh + (ks >> 1)))) & 0xFF);  // group 2 fh + ks / 2
-      }
-    // the first sub-step's x fragments too (the stage is complete since the last barrier)
-    bf16x8_t af[2][FI];
+      for (int i = 0; i < FI; ++i) af[ks][i] = *(const bf16x8_t *)(st + xo[ks] + 4096 * i);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (DMA) issue(s + 2);
+    // W sub-step ks, fragment j: 8 nvfp4 elements times the E4M3 scale of group 2 fh + ks / 2
+    bf16x8_t bf[4][FJ];
+    auto deq = [&](int ks, int j) __attribute__((always_inline)) {
+      const uint32_t word = ks == 0 ? wq[j].x : ks == 1 ? wq[j].y : ks == 2 ? wq[j].z : wq[j].w;
+      bf[ks][j] = deq8_nvfp4(word, (wsc[j] >> (8 * (2 * fh + (ks >> 1)))) & 0xFF);
+    };
 #pragma unroll
-    for (int i = 0; i < FI; ++i) af[0][i] = *(const bf16x8_t *)(st + oa[i] + 16 * ab[i]);  // ks = 0
+    for (int j = 0; j < FJ; ++j) deq(0, j);
+    // sub-step 0's W is pinned here, so that its VALU work stays in the loading interval
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) asm volatile("" : "+v"(bf[0][j]));
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (GRP == 0) gp_lds_barrier();
-    else if constexpr (DMA) gp_wait_barrier<G::DMA>();
-    else gp_wait_barrier<0>();
+    if constexpr (GRP == 0) gp_lds_barrier();  // ends interval 2s
+    else if constexpr (DMA) {                  // ends interval 2s + 1
+      if (sw) gp_wait_barrier<G::DMA_S>();
+      else gp_wait_barrier<G::DMA>();
+    } else {
+      gp_wait_barrier<0>();
+    }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (DMA && GRP == 0) issue(s + 2);  // interval 2s + 1
-    // computing interval: sub-step ks + 1's x fragments are read while sub-step
-    // ks's 2 FI MFMAs run
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       if (ks < 3) {
 #pragma unroll
-        for (int i = 0; i < FI; ++i)
-          af[(ks + 1) & 1][i] = *(const bf16x8_t *)(st + oa[i] + 16 * ((ks + 1) ^ ab[i]));
+        for (int j = 0; j < FJ; ++j) deq(ks + 1, j);
       }
 #pragma unroll
       for (int j = 0; j < FJ; ++j)
 #pragma unroll
         for (int i = 0; i < FI; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bf[ks][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
     }
-    // keep that order: the scheduler would otherwise sink each read next to its use
 #pragma unroll
-    for (int ks = 0; ks < 3; ++ks) {
-      __builtin_amdgcn_sched_group_barrier(0x100, FI, 0);       // FI LDS reads (sub-step ks + 1)
-      __builtin_amdgcn_sched_group_barrier(0x008, FJ * FI, 0);  // then sub-step ks's MFMAs
+    for (int m = 0; m < 4 * FI * FJ; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then four VALU
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, FJ * FI, 0);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (GRP == 1) gp_lds_barrier();
-    else if constexpr (DMA) {
+    if constexpr (GRP == 1) gp_barrier_only();  // ends interval 2s + 2 (no LDS read in it)
+    else if constexpr (DMA) {                   // ends interval 2s + 1
       if (sw) gp_wait_barrier<G::DMA_S>();
       else gp_wait_barrier<G::DMA>();
     } else {

@@ -37,6 +37,15 @@ __device__ __forceinline__ void gp_dma16(const void *g, uint32_t l) {
 __device__ __forceinline__ void gp_dma4(const void *g, uint32_t l) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(l), "v"(g) : "memory", "m0");
 }
+// The same with the source as a wave-uniform base (SGPRs) plus a 32-bit lane offset.
+__device__ __forceinline__ void gp_dma16s(const void *base, uint32_t off, uint32_t l) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(off), "s"(base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void gp_dma4s(const void *base, uint32_t off, uint32_t l) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(l), "v"(off), "s"(base)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Wait until at most N of this wave's vector-memory operations are in flight and
