@@ -247,6 +247,21 @@ def test_prefill_matches_oracle(mode, M, N, K):
     assert ok, (fro, worst)
 
 
+# K of one to three 64-element steps: the pipelined GEMMs' ring prologue issues fewer
+# steps than it has stages (nvfp4 at every K here, mxfp8 at K = 128), as whole tiles
+# (M = 300) and as the short-x tile heights (M = 40, 100).
+@pytest.mark.parametrize("mode", ["mxfp8", "nvfp4"])
+@pytest.mark.parametrize("M,N,K", [(300, 300, 64), (300, 300, 128), (300, 300, 192), (40, 600, 128), (100, 520, 192)])
+def test_prefill_short_k(mode, M, N, K):
+    rng = np.random.default_rng(7 * M + N + K)
+    wq, s = rand_w(rng, mode, N, K)
+    xb = bf16(rng.standard_normal((M, K)))
+    y = run_qmm(mode, xb, wq, s)
+    ref = O.qmm(mode, xb, wq, s)
+    ok, fro, worst = O.check_tolerance(f32(y), f32(ref), **TOL)
+    assert ok, (fro, worst)
+
+
 # The pipelined prefill GEMMs on weights over every code (all E2M1 nibbles / every
 # finite E4M3 byte) and x with the edge groups: ragged N and M, several K steps,
 # and the down projection's K = 17408 (checked on a column sample).
