@@ -60,25 +60,6 @@ __device__ __forceinline__ int aswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 // r and r + 8, and r and r + 4 on 32 banks, would otherwise share them)
 __device__ __forceinline__ int wswz(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
 
-// 8 nvfp4 elements (one dword, lowest nibble first) times the E4M3 scale byte, as 8 bf16.
-__device__ __forceinline__ bf16x8_t deq8_nvfp4(uint32_t word, uint32_t scale_byte) {
-  const float sc = __builtin_amdgcn_cvt_f32_fp8((int)scale_byte, 0);
-  bf16x8_t r;
-  const f32x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 0);
-  const f32x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 1);
-  const f32x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 2);
-  const f32x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 3);
-  r[0] = (__bf16)(p0.x * sc);
-  r[1] = (__bf16)(p0.y * sc);
-  r[2] = (__bf16)(p1.x * sc);
-  r[3] = (__bf16)(p1.y * sc);
-  r[4] = (__bf16)(p2.x * sc);
-  r[5] = (__bf16)(p2.y * sc);
-  r[6] = (__bf16)(p3.x * sc);
-  r[7] = (__bf16)(p3.y * sc);
-  return r;
-}
-
 // Tile `bid` of the TM x 256 tiling of x rows [0, M) and W rows [n_begin, n_end)
 // (n_begin a multiple of 256), over the K steps [s_begin, s_end).  With `part` null the
 // tile's bf16 result goes to y; otherwise (a K range of a split tile) the fp32

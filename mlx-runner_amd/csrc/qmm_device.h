@@ -27,6 +27,27 @@ __device__ __forceinline__ uint4 load_stream16(const void *p) {
 }
 
 
+// 8 nvfp4 elements (one dword, lowest nibble first) times the E4M3 scale byte, as 8 bf16:
+// E2M1 -> f32, times the scale, -> bf16.  E2M1 x E4M3 has at most 6 significant bits, so
+// the product and its bf16 are exact (the bf16 MFMA then multiplies it with x exactly).
+__device__ __forceinline__ bf16x8_t deq8_nvfp4(uint32_t word, uint32_t scale_byte) {
+  const float sc = __builtin_amdgcn_cvt_f32_fp8((int)scale_byte, 0);
+  bf16x8_t r;
+  const f32x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 0);
+  const f32x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 1);
+  const f32x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 2);
+  const f32x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 3);
+  r[0] = (__bf16)(p0.x * sc);
+  r[1] = (__bf16)(p0.y * sc);
+  r[2] = (__bf16)(p1.x * sc);
+  r[3] = (__bf16)(p1.y * sc);
+  r[4] = (__bf16)(p2.x * sc);
+  r[5] = (__bf16)(p2.y * sc);
+  r[6] = (__bf16)(p3.x * sc);
+  r[7] = (__bf16)(p3.y * sc);
+  return r;
+}
+
 // E8M0 scale byte -> f32: 2^(X-127); X = 0 is the subnormal 2^-127; 0xFF -> NaN.
 __device__ __forceinline__ float e8m0_to_f32(uint32_t b) {
   uint32_t u = b << 23;

@@ -110,15 +110,17 @@ hipError_t launch_repack_scales(const uint8_t *s, int64_t N, int nb, uint32_t *o
 // scale bytes per row it repacks): 0 when it reads them as stored.
 int gemm_tiled_scale_bytes_per_row(const QmmArgs &a);
 
-// Whether a call runs on the decode kernels (x of at most QMV_MAX_M rows, and mxfp8 x of
-// up to 16 rows where the MFMA decode kernel takes it) rather than a prefill GEMM.  x of 5-8 rows that the MFMA decode kernels do not take (nvfp4; mxfp8 at
+// Whether a call runs on the decode kernels (x of at most QMV_MAX_M rows, and x of up to
+// 16 rows where the MFMA decode kernels take it: mxfp8 on the scaled MFMA, nvfp4 at
+// K = 5120 / 6144 on the dequantizing bf16-MFMA kernel) rather than a prefill GEMM.  x of
+// 5-8 rows that the MFMA decode kernels do not take (nvfp4; mxfp8 at
 // K = 17408 from 6 rows) runs on the pipelined GEMM's split tiles when the matrix is tall:
 // the other decode kernel is the unpacking GEMV, whose work grows with every row
 // (N = 17408, K = 5120, nvfp4: 40-62 us at 5-8 rows against 25 us; N = 5120, K = 17408,
 // mxfp8: 50-61 us against 47 us).
 inline bool qmm_on_decode(const QmmArgs &a) {
-  // (mxfp8 x of 9-16 rows on the MFMA decode kernel, where it takes the shape)
-  if (a.M > QMV_MAX_M) return a.M <= 16 && a.mode == MXFP8 && qmv_mfma_ok(a);
+  // (x of 9-16 rows on the MFMA decode kernels, where they take the shape)
+  if (a.M > QMV_MAX_M) return a.M <= 16 && qmv_mfma_ok(a);
   if (a.M <= 4 || a.N < 4096 || qmv_mfma_ok(a) || ((uintptr_t)a.x | (uintptr_t)a.w) & 15) return true;
   if (a.mode == MXFP8) return !(gemm_mxfp8_ok(a) && a.K % 128 == 0 && ((uintptr_t)a.s & 3) == 0);
   return !gemm_nvfp4_ok(a);

@@ -1,6 +1,7 @@
 // Decode GEMV on the gfx950 scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4, and
-// the 32x32x64 form for nvfp4 at M = 3-4): y[m, n] = sum_k x[m, k] * deq(W)[n, k]
-// for M = 1..4, bf16 x, K = 5120 or 17408.
+// the 32x32x64 form for nvfp4 at M = 3-8): y[m, n] = sum_k x[m, k] * deq(W)[n, k]
+// for x of a few rows (mxfp8 up to 16), bf16 x, K = 5120, 6144, 10240 or 17408.  nvfp4
+// x of 9-16 rows runs a dequantizing kernel on the bf16 MFMA (qmv_deq16_kernel, below).
 //
 // The shapes are mlx-runner's per-token qmm calls (src/model.zig:906-908
 // gate/up and :912 down, :929-944 q/k/v, :1066-1074, :1309 lm_head; M = 1
@@ -680,6 +681,121 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
   }
 }
 
+
+// nvfp4 x of 9-16 rows.  The scaled-MFMA forms above hold one block-diagonal A operand
+// per x row (or per 4 rows): past 8 rows they run out of registers.  Here W is
+// dequantized instead (E2M1 x E4M3 -> bf16, exact) and the bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16) takes all 16 x rows as its A rows, so the cost per unit is
+// the dequantization (~2 VALU ops per weight), the same for any x of up to 16 rows.
+// Work split as in qmv_mfma_kernel: one workgroup per CU owns a contiguous row range,
+// wave q owns the K slice [512 q, 512 q + 512) (K = Q slices, one pass), units are 16
+// rows x one slice, staged through the wave's LDS tile (1 KiB-contiguous loads).
+//   The 512 elements of a slice are taken in an order chosen for the tile: MFMA c
+// (of 16) gives lane group h the elements 128 h + 8 c + [0, 8), the same for x and W,
+// so the sum is unchanged.  Lane (n, h) then reads W row n's bytes [64 h, 64 h + 64)
+// of the unit (four 16-byte reads) and the E4M3 bytes 8 h .. 8 h + 7 of its 32 (the
+// scale of MFMA c is byte c / 2), and holds x row n's elements 512 q + 128 h + [0, 128)
+// as its 16 A operands for the whole call (64 registers; rows from M on are zero).
+//   Output lane (n, h), element v: x row 4 h + v, W row n.  Partial sums go to LDS per
+// (row block, x row, wave) and are summed over the waves in a fixed order.
+constexpr int QD_PITCH = 272;                     // tile row pitch (256 bytes + 16)
+constexpr int QD_TILE = 16 * QD_PITCH + 16 * 32;  // 16 rows of W + their 32 scale bytes
+constexpr int QD_FLUSH_MAX = 8;
+constexpr size_t qd_lds_bytes(int Q, int F) { return (size_t)Q * QD_TILE + (size_t)F * 16 * Q * 16 * 4; }
+
+template <int Q>
+__global__ __launch_bounds__(64 * Q) void qmv_deq16_kernel(int N, int K, int M, int F, int rbase, int rrem,
+                                                           const uint16_t *__restrict__ x,
+                                                           const uint8_t *__restrict__ w,
+                                                           const uint8_t *__restrict__ s, uint16_t *__restrict__ y) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
+  uint8_t *wt = lds + q * QD_TILE, *st = wt + 16 * QD_PITCH;
+  float *part = (float *)(lds + Q * QD_TILE);  // [F][16 x rows][Q][16 W rows] partial sums
+  const int r_begin = rows_begin(blockIdx.x, rbase, rrem);
+  const int r_end = rows_begin(blockIdx.x + 1, rbase, rrem);
+  const int nrb = (r_end - r_begin + 15) / 16;
+  const int n = lane & 15, h = lane >> 4;
+
+  // 1) x: the A operands of the slice's 16 MFMAs (rows from M on: zero)
+  bf16x8_t af[16];
+  {
+    const bool live = n < M;
+    const uint4 *xp = (const uint4 *)(x + (int64_t)(live ? n : 0) * K + 512 * q + 128 * h);
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      uint4 v = xp[c];
+      if (!live) v = make_uint4(0, 0, 0, 0);
+      af[c] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2) units.  Load i (of 4), lane l: row 4 i + l / 16 of the block, bytes 16 (l % 16) of the
+  //    slice's 256; scales: lane l, row l / 4, bytes 8 (l % 4) of the slice's 32.  Rows past
+  //    the range re-read its last row (results dropped); W offsets are 32-bit (the host
+  //    checks that the matrix is under 4 GiB).
+  const uint32_t wrow = (uint32_t)(K >> 1), srow = (uint32_t)(K >> 4);
+  auto row_of = [&](int rb, int rr) __attribute__((always_inline)) {
+    const int row = r_begin + 16 * rb + rr;
+    return (uint32_t)(row < r_end ? row : r_end - 1);
+  };
+  uint4 wv[4];
+  uint2 sv;
+  auto load_unit = [&](int rb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wv[i] = load_stream16(w + row_of(rb, 4 * i + (lane >> 4)) * wrow + 256 * q + 16 * (lane & 15));
+    sv = *(const uint2 *)(s + row_of(rb, lane >> 2) * srow + 32 * q + 8 * (lane & 3));
+  };
+  load_unit(0);
+
+  // sum the waves' partials of row blocks [rb_first, rb_last] in wave order
+  auto flush = [&](int rb_first, int rb_last) __attribute__((always_inline)) {
+    lds_barrier();
+    const int items = (rb_last - rb_first + 1) * M * 16;
+    for (int t = tid; t < items; t += 64 * Q) {
+      const int nn = t & 15, m = (t >> 4) % M, rbi = t / (16 * M);
+      const int row = r_begin + 16 * (rb_first + rbi) + nn;
+      const float *pp = part + ((rbi * 16 + m) * Q) * 16 + nn;
+      float sum = 0.f;
+#pragma unroll
+      for (int qq = 0; qq < Q; ++qq) sum += pp[16 * qq];
+      if (row < r_end) y[(int64_t)m * N + row] = f32_to_bf16_rne(sum);
+    }
+    lds_barrier();
+  };
+
+  // a do-while: every workgroup has a row block
+  int rb = 0, rbf = 0;  // rbf = rb % F, kept by a counter
+  do {
+    // unit rb: registers -> tile, then refill them with unit rb + 1 (past the last: clamped
+    // rows, unused).  One wave's LDS accesses run in order: the reads below see this unit.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(uint4 *)(wt + (4 * i + (lane >> 4)) * QD_PITCH + 16 * (lane & 15)) = wv[i];
+    *(uint2 *)(st + 8 * lane) = sv;
+    load_unit(rb + 1);
+    uint4 wq[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wq[i] = *(const uint4 *)(wt + n * QD_PITCH + 64 * h + 16 * i);
+    const uint2 sc8 = *(const uint2 *)(st + n * 32 + 8 * h);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const uint4 &u = wq[c >> 2];
+      const uint32_t word = (c & 3) == 0 ? u.x : (c & 3) == 1 ? u.y : (c & 3) == 2 ? u.z : u.w;
+      const uint32_t sb = ((c >> 1) < 4 ? sc8.x >> (8 * (c >> 1)) : sc8.y >> (8 * ((c >> 1) - 4))) & 0xFF;
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[c], deq8_nvfp4(word, sb), acc, 0, 0, 0);
+    }
+    float *pslot = part + (rbf * 16) * Q * 16;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 4 * h + v;
+      if (m < M) pslot[(m * Q + q) * 16 + n] = acc[v];
+    }
+    if (rbf + 1 == F || rb + 1 == nrb) flush(rb - rbf, rb);
+    rbf = rbf + 1 == F ? 0 : rbf + 1;
+  } while (++rb < nrb);
+}
 }  // namespace
 
 // Waves per workgroup (Q) and passes (P) for K, the model's row lengths:
@@ -722,7 +838,20 @@ static int qf_flush_rows(const QmmArgs &a, int nrb) {
 
 static bool q32_ok(const QmmArgs &a);
 
+// nvfp4 x of 9-16 rows on the dequantizing kernel: K of one pass (5120: Q = 10, 6144: Q = 12).
+static bool qd_ok(const QmmArgs &a) {
+  if (a.mode != NVFP4 || a.x_f32 || a.M < 9 || a.M > 16 || a.N < 16) return false;
+  const QfShape g = qf_shape(a.K);
+  if (g.Q == 0 || g.P != 1 || qf_cus() == 0) return false;
+  if ((int64_t)a.N * (a.K / 2) >= ((int64_t)1 << 32)) return false;  // 32-bit offsets within W
+  return ((((uintptr_t)a.x) | ((uintptr_t)a.w)) & 15) == 0 && ((uintptr_t)a.s & 7) == 0;
+}
+
 bool qmv_mfma_ok(const QmmArgs &a) {
+  // nvfp4 x of 9-16 rows: the dequantizing kernel (N = 17408, K = 5120: 16.0-17.9 us at
+  // 9-16 rows against 24.9-25.5 us on the prefill GEMM's split tiles; N = 5120, K = 6144:
+  // 9.6-11.7 against 15.1-15.4)
+  if (a.mode == NVFP4 && a.M > 8) return qd_ok(a);
   // (mxfp8 holds x rows as A columns (m, hi|lo): 16 columns per operand, 8 rows, and two
   // operands per chunk for 9-16 rows; nvfp4 runs 3-8 rows on the 32x32x64 form, two
   // operands per chunk from 5 rows)
@@ -933,15 +1062,44 @@ static hipError_t launch_q32_mlp(const QmmArgs &a, const uint8_t *w_up, const ui
   return launch_q32<4, 10, 1, 2>(a, w_up, s_up, grid, F, st);
 }
 
+// Row blocks per partial-sum flush of the dequantizing kernel: as many as fit the LDS.
+static int qd_flush_rows(int nrb, int Q) {
+  int F = nrb < QD_FLUSH_MAX ? nrb : QD_FLUSH_MAX;
+  while (F > 1 && qd_lds_bytes(Q, F) > QF_LDS_MAX) --F;
+  return F;
+}
+
+template <int Q>
+static hipError_t launch_qd(const QmmArgs &a, int grid, int F, hipStream_t st) {
+  auto kern = qmv_deq16_kernel<Q>;
+  static std::atomic<uint64_t> lds_set{0};
+  const hipError_t e = ensure_dynamic_lds(lds_set, (const void *)kern, 160 * 1024);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), qd_lds_bytes(Q, F), st, a.N, a.K, a.M, F, a.N / grid,
+                     a.N % grid, (const uint16_t *)a.x, a.w, a.s, (uint16_t *)a.y);
+  return hipGetLastError();
+}
+
+static hipError_t launch_qd_any(const QmmArgs &a, hipStream_t st) {
+  if (!qd_ok(a) || a.parts) return hipErrorInvalidValue;
+  const int cus = qf_cus();
+  const int rbs = (a.N + 15) / 16;
+  const int grid = rbs < cus ? rbs : cus;
+  const int Q = qf_shape(a.K).Q;
+  const int F = qd_flush_rows(qf_nrb(a, cus), Q);
+  return Q == 12 ? launch_qd<12>(a, grid, F, st) : launch_qd<10>(a, grid, F, st);
+}
+
 hipError_t launch_qmv_mfma(const QmmArgs &a, hipStream_t st) {
   if (!qmv_mfma_ok(a)) return hipErrorInvalidValue;
+  if (a.mode == NVFP4 && a.M > 8) return launch_qd_any(a, st);
   if (a.mode == NVFP4 && a.M > 2) return launch_q32_any(a, st);
   if (a.parts) return a.K == 5120 ? launch_qf_any<1, true>(a, a.w, a.s, st) : hipErrorInvalidValue;
   return launch_qf_any<1>(a, a.w, a.s, st);
 }
 
-// Grouped calls on these kernels: K = 5120.
-bool qmv_mfma_parts_ok(const QmmArgs &a) { return qmv_mfma_ok(a) && a.K == 5120; }
+// Grouped calls on these kernels: K = 5120 (not the dequantizing kernel).
+bool qmv_mfma_parts_ok(const QmmArgs &a) { return qmv_mfma_ok(a) && a.K == 5120 && !(a.mode == NVFP4 && a.M > 8); }
 
 hipError_t launch_qmv_mfma_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st) {
   if (!qmv_mfma_mlp_ok(a, w_up, s_up)) return hipErrorInvalidValue;

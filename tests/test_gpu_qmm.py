@@ -394,7 +394,9 @@ def make_x(rng, M, K, kind):
 # nvfp4 M = 3-4 runs the 32x32x64 form (32-row blocks, flushes every 4 blocks);
 # mxfp8 M = 5-8 the 16x16x128 form with all 16 A columns (8 rows x hi|lo) live, M = 9-16
 # with two A operands per chunk (their records made 8 rows at a time); nvfp4 M = 5-8 the
-# 32x32x64 form with two A operands per chunk (rows 4 G + [0, 4) in operand G).
+# 32x32x64 form with two A operands per chunk (rows 4 G + [0, 4) in operand G); nvfp4
+# M = 9-16 the dequantizing kernel (W -> bf16, all 16 x rows on the bf16 MFMA), down to
+# N = 100 (7 workgroups of 14-15 rows).
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 1, 70001), ("nvfp4", 2, 4099),
                                       ("nvfp4", 2, 16384), ("nvfp4", 3, 4099), ("nvfp4", 3, 70001),
                                       ("nvfp4", 4, 16400), ("mxfp8", 2, 4101), ("mxfp8", 3, 8192),
@@ -402,7 +404,8 @@ def make_x(rng, M, K, kind):
                                       ("mxfp8", 6, 8192), ("mxfp8", 7, 4096), ("mxfp8", 8, 70001),
                                       ("mxfp8", 9, 4101), ("mxfp8", 12, 8192), ("mxfp8", 15, 4096),
                                       ("mxfp8", 16, 70001), ("nvfp4", 5, 4099), ("nvfp4", 6, 70001),
-                                      ("nvfp4", 7, 5120), ("nvfp4", 8, 16400)])
+                                      ("nvfp4", 7, 5120), ("nvfp4", 8, 16400), ("nvfp4", 9, 4099),
+                                      ("nvfp4", 12, 70001), ("nvfp4", 16, 16400), ("nvfp4", 13, 100)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
 def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
     K = 5120
@@ -449,7 +452,8 @@ def test_decode_mfma_down_shapes_match_oracle(mode, M, N, xkind):
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 5120), ("nvfp4", 2, 4099), ("nvfp4", 3, 5120),
                                       ("nvfp4", 4, 4099), ("mxfp8", 2, 5120), ("mxfp8", 3, 4101),
                                       ("mxfp8", 4, 8192), ("mxfp8", 6, 5120), ("mxfp8", 8, 4101),
-                                      ("mxfp8", 13, 5120), ("mxfp8", 16, 4101), ("nvfp4", 6, 4099)])
+                                      ("mxfp8", 13, 5120), ("mxfp8", 16, 4101), ("nvfp4", 6, 4099),
+                                      ("nvfp4", 10, 5120), ("nvfp4", 16, 4099)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
 def test_decode_mfma_other_k_match_oracle(K, mode, M, N, xkind):
     rng = np.random.default_rng(N * 10 + M + K)
