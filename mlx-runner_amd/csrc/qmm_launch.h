@@ -112,7 +112,7 @@ int gemm_tiled_scale_bytes_per_row(const QmmArgs &a);
 
 // Whether a call runs on the decode kernels (x of at most QMV_MAX_M rows, and x of up to
 // 16 rows where the MFMA decode kernels take it: mxfp8 on the scaled MFMA, nvfp4 at
-// K = 5120 / 6144 on the dequantizing bf16-MFMA kernel) rather than a prefill GEMM.  x of
+// K = 5120 / 6144 from 5 rows on the dequantizing bf16-MFMA kernel) rather than a prefill GEMM.  x of
 // 5-8 rows that the MFMA decode kernels do not take (nvfp4; mxfp8 at
 // K = 17408 from 6 rows) runs on the pipelined GEMM's split tiles when the matrix is tall:
 // the other decode kernel is the unpacking GEMV, whose work grows with every row

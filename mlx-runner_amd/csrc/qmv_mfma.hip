@@ -1,7 +1,8 @@
 // Decode GEMV on the gfx950 scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4, and
 // the 32x32x64 form for nvfp4 at M = 3-8): y[m, n] = sum_k x[m, k] * deq(W)[n, k]
 // for x of a few rows (mxfp8 up to 16), bf16 x, K = 5120, 6144, 10240 or 17408.  nvfp4
-// x of 9-16 rows runs a dequantizing kernel on the bf16 MFMA (qmv_deq16_kernel, below).
+// x of 5-16 rows at K = 5120 / 6144 runs a dequantizing kernel on the bf16 MFMA
+// (qmv_deq16_kernel, below).
 //
 // The shapes are mlx-runner's per-token qmm calls (src/model.zig:906-908
 // gate/up and :912 down, :929-944 q/k/v, :1066-1074, :1309 lm_head; M = 1
@@ -543,9 +544,9 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
   };
   load_unit(0, 0);
 
-  // A operands of the slice's 8 chunks (see above), from the x records; x of 5-8 rows
-  // takes two operands per chunk, operand G holding rows 4 G + [0, 4)
-  constexpr int MG = (M + 3) / 4;
+  // A operands of the slice's 8 chunks (see above), from the x records: one per chunk
+  static_assert(M <= 4, "x of up to 4 rows (one A operand per chunk)");
+  constexpr int MG = 1;
   const int i = lane & 31, h = lane >> 5;
   const int am = i >> 3, ag = (i >> 1) & 3, ahl = i & 1;
   // A lane (i, h) is nonzero in bytes 0-15 (own0) or 16-31 (own1) or nowhere, the
@@ -646,14 +647,8 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
           const uint4 ad = areg[c8][G];
           const i32x8_t aw = {(int)(ad.x & k0), (int)(ad.y & k0), (int)(ad.z & k0), (int)(ad.w & k0),
                               (int)(ad.x & k1), (int)(ad.y & k1), (int)(ad.z & k1), (int)(ad.w & k1)};
-          int bg0 = bw[0];
-          if constexpr (MG > 1) {  // operand G's MFMA after operand G - 1's sums (one output live)
-#pragma unroll
-            for (int m = 0; m < M; ++m) asm volatile("" : "+v"(bg0) : "v"(acc[m]));
-          }
-          const i32x8_t bwg = {bg0, bw[1], bw[2], bw[3], 0, 0, 0, 0};
           const f32x16_t dd = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-              aw, bwg, f32x16_t{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, 0, 4,
+              aw, bw, f32x16_t{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, 0, 4,
               0, asreg[c8][G], 0, 127);
 #pragma unroll
           for (int mm = 0; mm < 4; ++mm) {
@@ -682,8 +677,9 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
 }
 
 
-// nvfp4 x of 9-16 rows.  The scaled-MFMA forms above hold one block-diagonal A operand
-// per x row (or per 4 rows): past 8 rows they run out of registers.  Here W is
+// nvfp4 x of 5-16 rows.  The scaled-MFMA forms above hold one block-diagonal A operand
+// per x row (or per 4 rows): past 8 rows they run out of registers, and from 5 rows their
+// MFMA and scaling work per unit grows with every row.  Here W is
 // dequantized instead (E2M1 x E4M3 -> bf16, exact) and the bf16 MFMA
 // (v_mfma_f32_16x16x32_bf16) takes all 16 x rows as its A rows, so the cost per unit is
 // the dequantization (~2 VALU ops per weight), the same for any x of up to 16 rows.
@@ -838,9 +834,12 @@ static int qf_flush_rows(const QmmArgs &a, int nrb) {
 
 static bool q32_ok(const QmmArgs &a);
 
-// nvfp4 x of 9-16 rows on the dequantizing kernel: K of one pass (5120: Q = 10, 6144: Q = 12).
+// nvfp4 x of 5-16 rows on the dequantizing kernel: K of one pass (5120: Q = 10, 6144: Q = 12).
 static bool qd_ok(const QmmArgs &a) {
-  if (a.mode != NVFP4 || a.x_f32 || a.M < 9 || a.M > 16 || a.N < 16) return false;
+  if (a.mode != NVFP4 || a.x_f32 || a.M < 5 || a.M > 16 || a.N < 16) return false;
+  // at 5-8 rows the unpacking GEMV stays ahead on short matrices (N = 48: 5.0 against
+  // 5.9 us at M = 5; N = 1024: 6.7 against 6.1)
+  if (a.M <= 8 && a.N < 1024) return false;
   const QfShape g = qf_shape(a.K);
   if (g.Q == 0 || g.P != 1 || qf_cus() == 0) return false;
   if ((int64_t)a.N * (a.K / 2) >= ((int64_t)1 << 32)) return false;  // 32-bit offsets within W
@@ -848,10 +847,11 @@ static bool qd_ok(const QmmArgs &a) {
 }
 
 bool qmv_mfma_ok(const QmmArgs &a) {
-  // nvfp4 x of 9-16 rows: the dequantizing kernel (N = 17408, K = 5120: 16.0-17.9 us at
-  // 9-16 rows against 24.9-25.5 us on the prefill GEMM's split tiles; N = 5120, K = 6144:
-  // 9.6-11.7 against 15.1-15.4)
-  if (a.mode == NVFP4 && a.M > 8) return qd_ok(a);
+  // nvfp4 x of 5-16 rows at K = 5120 / 6144: the dequantizing kernel (N = 17408, K = 5120:
+  // 14.9-15.5 us at 5-8 rows against 17.1-19.3 on the 32x32x64 form, 16.0-17.9 us at 9-16
+  // rows against 24.9-25.5 on the prefill GEMM's split tiles)
+  if (a.mode == NVFP4 && a.M >= 5 && qd_ok(a)) return true;
+  if (a.mode == NVFP4 && a.M > 8) return false;
   // (mxfp8 holds x rows as A columns (m, hi|lo): 16 columns per operand, 8 rows, and two
   // operands per chunk for 9-16 rows; nvfp4 runs 3-8 rows on the 32x32x64 form, two
   // operands per chunk from 5 rows)
@@ -998,10 +998,11 @@ static int q32_flush_rows(const QmmArgs &a, int nrb) {
 }
 
 static bool q32_ok(const QmmArgs &a) {
-  if (a.mode != NVFP4 || a.x_f32 || a.M < 1 || a.M > 8 || a.N < 16) return false;
+  // (x of 5-8 rows at K = 5120 / 6144 runs the dequantizing kernel, faster than this form's
+  // two A operands per chunk from N = 1024)
+  if (a.mode != NVFP4 || a.x_f32 || a.M < 1 || a.M > 4 || a.N < 16) return false;
   const QfShape g = qf_shape(a.K);
   if (g.Q == 0 || qf_cus() == 0) return false;
-  if (a.M > 4 && g.P > 1) return false;  // x of 5-8 rows: one pass (two A operands per chunk)
   if (g.P > 1 && q32_flush_rows(a, q32_nrb(a, qf_cus())) < q32_nrb(a, qf_cus())) return false;
   if ((int64_t)a.N * (a.K / 2) >= ((int64_t)1 << 32)) return false;  // 32-bit offsets within W
   return ((((uintptr_t)a.x) | ((uintptr_t)a.w) | ((uintptr_t)a.s)) & 15) == 0;
@@ -1010,12 +1011,8 @@ static bool q32_ok(const QmmArgs &a) {
 // the plain 32-row form for K's (Q, P)
 template <int M>
 static hipError_t launch_q32_k(const QmmArgs &a, QfShape g, int grid, int F, hipStream_t st) {
-  if constexpr (M <= 4) {
-    if (g.P == 3) return launch_q32<M, 12, 3, 1>(a, a.w, a.s, grid, F, st);
-    if (g.P == 2) return launch_q32<M, 10, 2, 1>(a, a.w, a.s, grid, F, st);
-  } else if (g.P > 1) {
-    return hipErrorInvalidValue;
-  }
+  if (g.P == 3) return launch_q32<M, 12, 3, 1>(a, a.w, a.s, grid, F, st);
+  if (g.P == 2) return launch_q32<M, 10, 2, 1>(a, a.w, a.s, grid, F, st);
   if (g.Q == 12) return launch_q32<M, 12, 1, 1>(a, a.w, a.s, grid, F, st);
   return launch_q32<M, 10, 1, 1>(a, a.w, a.s, grid, F, st);
 }
@@ -1038,11 +1035,7 @@ static hipError_t launch_q32_any(const QmmArgs &a, hipStream_t st) {
     case 1: return launch_q32_k<1>(a, g, grid, F, st);
     case 2: return launch_q32_k<2>(a, g, grid, F, st);
     case 3: return launch_q32_k<3>(a, g, grid, F, st);
-    case 4: return launch_q32_k<4>(a, g, grid, F, st);
-    case 5: return launch_q32_k<5>(a, g, grid, F, st);
-    case 6: return launch_q32_k<6>(a, g, grid, F, st);
-    case 7: return launch_q32_k<7>(a, g, grid, F, st);
-    default: return launch_q32_k<8>(a, g, grid, F, st);
+    default: return launch_q32_k<4>(a, g, grid, F, st);
   }
 }
 
@@ -1092,14 +1085,14 @@ static hipError_t launch_qd_any(const QmmArgs &a, hipStream_t st) {
 
 hipError_t launch_qmv_mfma(const QmmArgs &a, hipStream_t st) {
   if (!qmv_mfma_ok(a)) return hipErrorInvalidValue;
-  if (a.mode == NVFP4 && a.M > 8) return launch_qd_any(a, st);
+  if (a.mode == NVFP4 && a.M >= 5 && qd_ok(a)) return launch_qd_any(a, st);
   if (a.mode == NVFP4 && a.M > 2) return launch_q32_any(a, st);
   if (a.parts) return a.K == 5120 ? launch_qf_any<1, true>(a, a.w, a.s, st) : hipErrorInvalidValue;
   return launch_qf_any<1>(a, a.w, a.s, st);
 }
 
 // Grouped calls on these kernels: K = 5120 (not the dequantizing kernel).
-bool qmv_mfma_parts_ok(const QmmArgs &a) { return qmv_mfma_ok(a) && a.K == 5120 && !(a.mode == NVFP4 && a.M > 8); }
+bool qmv_mfma_parts_ok(const QmmArgs &a) { return qmv_mfma_ok(a) && a.K == 5120 && !(a.mode == NVFP4 && a.M > 4); }
 
 hipError_t launch_qmv_mfma_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st) {
   if (!qmv_mfma_mlp_ok(a, w_up, s_up)) return hipErrorInvalidValue;

@@ -394,9 +394,8 @@ def make_x(rng, M, K, kind):
 # nvfp4 M = 3-4 runs the 32x32x64 form (32-row blocks, flushes every 4 blocks);
 # mxfp8 M = 5-8 the 16x16x128 form with all 16 A columns (8 rows x hi|lo) live, M = 9-16
 # with two A operands per chunk (their records made 8 rows at a time); nvfp4 M = 5-8 the
-# 32x32x64 form with two A operands per chunk (rows 4 G + [0, 4) in operand G); nvfp4
-# M = 9-16 the dequantizing kernel (W -> bf16, all 16 x rows on the bf16 MFMA), down to
-# N = 100 (7 workgroups of 14-15 rows).
+# dequantizing kernel (W -> bf16, all 16 x rows on the bf16 MFMA), as nvfp4 M = 9-16, down
+# to N = 100 (7 workgroups of 14-15 rows).
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 1, 70001), ("nvfp4", 2, 4099),
                                       ("nvfp4", 2, 16384), ("nvfp4", 3, 4099), ("nvfp4", 3, 70001),
                                       ("nvfp4", 4, 16400), ("mxfp8", 2, 4101), ("mxfp8", 3, 8192),

@@ -150,8 +150,9 @@ FAMILIES = [
     ("nvfp4", 2, 4099, 5120, "bf16"),     # scaled-MFMA GEMV, M = 2
     ("nvfp4", 3, 4099, 5120, "bf16"),     # 32x32x64 MFMA GEMV, one pass
     ("nvfp4", 3, 5120, 17408, "bf16"),    # 32x32x64 MFMA GEMV, several passes
-    ("nvfp4", 6, 1024, 5120, "bf16"),     # unpacking GEMV, M = 6
-    ("nvfp4", 12, 4099, 5120, "bf16"),    # dequantizing bf16-MFMA GEMV, x of 9-16 rows
+    ("nvfp4", 6, 512, 5120, "bf16"),      # unpacking GEMV, M = 6
+    ("nvfp4", 6, 4099, 5120, "bf16"),     # dequantizing bf16-MFMA GEMV, x of 5-8 rows
+    ("nvfp4", 12, 4099, 5120, "bf16"),    # the same, x of 9-16 rows
     ("nvfp4", 16, 1024, 6144, "bf16"),    # the same at K = 6144 (12 waves)
     ("nvfp4", 300, 1000, 1024, "bf16"),   # prefill GEMM on the bf16 MFMA
     ("nvfp4", 2, 512, 1024, "f32"),       # f32 x GEMV
