@@ -87,7 +87,7 @@ bool qmv_mlp_ok(const QmmArgs &a);
 hipError_t launch_qmv_mlp(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up, hipStream_t st);
 hipError_t launch_silu_mul(const void *g, const void *u, void *h, int64_t n, bool f32, hipStream_t st);
 
-// Prefill GEMM (M > QMV_MAX_M, and nvfp4 at 5-8 rows: qmm_on_decode).
+// Prefill GEMM (M > QMV_MAX_M, and 5-8 rows the decode MFMA kernels do not take: qmm_on_decode).
 bool gemm_ok(const QmmArgs &a);
 hipError_t launch_gemm(const QmmArgs &a, hipStream_t st);
 
@@ -113,7 +113,7 @@ int gemm_tiled_scale_bytes_per_row(const QmmArgs &a);
 // Whether a call runs on the decode kernels (x of at most QMV_MAX_M rows, and x of up to
 // 16 rows where the MFMA decode kernels take it: mxfp8 on the scaled MFMA, nvfp4 at
 // K = 5120 / 6144 from 5 rows on the dequantizing bf16-MFMA kernel) rather than a prefill GEMM.  x of
-// 5-8 rows that the MFMA decode kernels do not take (nvfp4; mxfp8 at
+// 5-8 rows that the MFMA decode kernels do not take (nvfp4 at K = 10240 / 17408; mxfp8 at
 // K = 17408 from 6 rows) runs on the pipelined GEMM's split tiles when the matrix is tall:
 // the other decode kernel is the unpacking GEMV, whose work grows with every row
 // (N = 17408, K = 5120, nvfp4: 40-62 us at 5-8 rows against 25 us; N = 5120, K = 17408,
