@@ -492,7 +492,11 @@ constexpr size_t q32_lds_bytes(int M, int Q, int F) { return (size_t)Q * Q32_WAV
 
 // NMAT = 2: the MLP form, a unit's 32 columns being 16 rows of W (gate) and the
 // same 16 rows of W2 (up); the flush writes silu(gate) * up (as in qmv_mfma_kernel).
-template <int M, int Q, int P, int NMAT, bool PARTS = false>
+//
+// LU < 8 (one row block per workgroup, at most 4 LU rows): the unit's loads of rows past
+// the range, which every unit would make and whose sums are dropped, are not made (tile
+// rows 4 LU .. 31 keep stale bytes, which reach only the dropped output rows).
+template <int M, int Q, int P, int NMAT, bool PARTS = false, int LU = 8>
 __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F, int rbase, int rrem,
                                                             const uint16_t *__restrict__ x,
                                                             const uint8_t *__restrict__ w,
@@ -532,10 +536,11 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
   // unit (pass, rb); row blocks past the range read clamped rows (unused).
   // W and scale addresses are 32-bit offsets (the host checks that a matrix is under 4 GiB).
   const uint8_t *sbase = NMAT == 2 && lane >= 32 ? s2 : s;  // this lane's scale rows
+  static_assert(LU == 8 || (NMAT == 1 && LU >= 1 && LU < 8), "rows per unit");
   auto load_unit = [&](int pass, int rb) __attribute__((always_inline)) {
     const int sl = slice_of(pass);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < LU; ++i) {
       const uint8_t *wm = NMAT == 2 && i >= 4 ? w2 : w;  // a load's rows are all in one matrix
       wv[i] = load_stream16(wm + ((uint32_t)row_of(rb, 4 * i + (lane >> 4)) * (uint32_t)wrow + sl * 256 +
                                   16 * (lane & 15)));
@@ -619,7 +624,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
       // unit (p, rb): registers -> tile (the x records are no longer needed there), then
       // refill the registers with the next unit (past the last one: clamped, unused)
 #pragma unroll
-      for (int li = 0; li < 8; ++li) *(uint4 *)(wt + (4 * li + (lane >> 4)) * Q32_PITCH + 16 * (lane & 15)) = wv[li];
+      for (int li = 0; li < LU; ++li) *(uint4 *)(wt + (4 * li + (lane >> 4)) * Q32_PITCH + 16 * (lane & 15)) = wv[li];
       *(uint4 *)(st + 16 * lane) = sv;
       // the next unit: this pass's next row block or the next pass's first; after the
       // last pass's last unit the clamped rows past the range (one row, cached)
@@ -971,10 +976,10 @@ static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8
 }
 
 // nvfp4 on the 32x32x64 form: 32-row blocks, one unit in flight per wave.
-template <int M, int Q, int P, int NMAT, bool PARTS = false>
+template <int M, int Q, int P, int NMAT, bool PARTS = false, int LU = 8>
 static hipError_t launch_q32(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
                              hipStream_t st) {
-  auto kern = qmv_mfma32_kernel<M, Q, P, NMAT, PARTS>;
+  auto kern = qmv_mfma32_kernel<M, Q, P, NMAT, PARTS, LU>;
   static std::atomic<uint64_t> lds_set{0};
   const hipError_t e = ensure_dynamic_lds(lds_set, (const void *)kern, 160 * 1024);
   if (e != hipSuccess) return e;
@@ -1011,7 +1016,16 @@ static bool q32_ok(const QmmArgs &a) {
 // the plain 32-row form for K's (Q, P)
 template <int M>
 static hipError_t launch_q32_k(const QmmArgs &a, QfShape g, int grid, int F, hipStream_t st) {
-  if (g.P == 3) return launch_q32<M, 12, 3, 1>(a, a.w, a.s, grid, F, st);
+  if (g.P == 3) {
+    // K = 17408 (the down projection): at most 28 rows per workgroup load only those rows
+    const int rows = a.N / grid + (a.N % grid ? 1 : 0), lu = (rows + 3) / 4;
+    if constexpr (M >= 3) {
+      if (lu <= 5) return launch_q32<M, 12, 3, 1, false, 5>(a, a.w, a.s, grid, F, st);
+      if (lu == 6) return launch_q32<M, 12, 3, 1, false, 6>(a, a.w, a.s, grid, F, st);
+      if (lu == 7) return launch_q32<M, 12, 3, 1, false, 7>(a, a.w, a.s, grid, F, st);
+    }
+    return launch_q32<M, 12, 3, 1>(a, a.w, a.s, grid, F, st);
+  }
   if (g.P == 2) return launch_q32<M, 10, 2, 1>(a, a.w, a.s, grid, F, st);
   if (g.Q == 12) return launch_q32<M, 12, 1, 1>(a, a.w, a.s, grid, F, st);
   return launch_q32<M, 10, 1, 1>(a, a.w, a.s, grid, F, st);
