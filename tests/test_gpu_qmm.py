@@ -423,8 +423,9 @@ def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
 # passes, the last pass with 2 slices past K.  The edge groups are planted in
 # the first slice of every pass and in the last slice.
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 5120), ("nvfp4", 2, 4099), ("nvfp4", 3, 5120),
-                                      ("nvfp4", 4, 4099), ("mxfp8", 2, 5120), ("mxfp8", 3, 4101),
-                                      ("mxfp8", 4, 8192), ("mxfp8", 5, 5120), ("mxfp8", 6, 4101),
+                                      ("nvfp4", 4, 4099), ("mxfp8", 1, 5120), ("mxfp8", 1, 4101),
+                                      ("mxfp8", 2, 5120), ("mxfp8", 3, 4101), ("mxfp8", 4, 8192),
+                                      ("mxfp8", 5, 5120), ("mxfp8", 6, 4101),
                                       ("mxfp8", 10, 5120), ("nvfp4", 7, 5120)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
 def test_decode_mfma_down_shapes_match_oracle(mode, M, N, xkind):
@@ -449,8 +450,9 @@ def test_decode_mfma_down_shapes_match_oracle(mode, M, N, xkind):
 # the last slice.
 @pytest.mark.parametrize("K", [6144, 10240])
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 5120), ("nvfp4", 2, 4099), ("nvfp4", 3, 5120),
-                                      ("nvfp4", 4, 4099), ("mxfp8", 2, 5120), ("mxfp8", 3, 4101),
-                                      ("mxfp8", 4, 8192), ("mxfp8", 6, 5120), ("mxfp8", 8, 4101),
+                                      ("nvfp4", 4, 4099), ("mxfp8", 1, 5120), ("mxfp8", 1, 4101),
+                                      ("mxfp8", 2, 5120), ("mxfp8", 3, 4101), ("mxfp8", 4, 8192),
+                                      ("mxfp8", 6, 5120), ("mxfp8", 8, 4101),
                                       ("mxfp8", 13, 5120), ("mxfp8", 16, 4101), ("nvfp4", 6, 4099),
                                       ("nvfp4", 10, 5120), ("nvfp4", 16, 4099)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
