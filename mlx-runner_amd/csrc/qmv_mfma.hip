@@ -1017,22 +1017,25 @@ static bool q32_ok(const QmmArgs &a) {
   return ((((uintptr_t)a.x) | ((uintptr_t)a.w) | ((uintptr_t)a.s)) & 15) == 0;
 }
 
-// the plain 32-row form for K's (Q, P)
+// the plain 32-row form for K's (Q, P), with the loads a unit makes: at most 28 rows
+// per workgroup (one row block; 5120 rows: 20) load only those rows
+template <int M, int Q, int P>
+static hipError_t launch_q32_lu(const QmmArgs &a, int grid, int F, hipStream_t st) {
+  const int rows = a.N / grid + (a.N % grid ? 1 : 0), lu = (rows + 3) / 4;
+  if constexpr (M >= 3) {
+    if (lu <= 5) return launch_q32<M, Q, P, 1, false, 5>(a, a.w, a.s, grid, F, st);
+    if (lu == 6) return launch_q32<M, Q, P, 1, false, 6>(a, a.w, a.s, grid, F, st);
+    if (lu == 7) return launch_q32<M, Q, P, 1, false, 7>(a, a.w, a.s, grid, F, st);
+  }
+  return launch_q32<M, Q, P, 1>(a, a.w, a.s, grid, F, st);
+}
+
 template <int M>
 static hipError_t launch_q32_k(const QmmArgs &a, QfShape g, int grid, int F, hipStream_t st) {
-  if (g.P == 3) {
-    // K = 17408 (the down projection): at most 28 rows per workgroup load only those rows
-    const int rows = a.N / grid + (a.N % grid ? 1 : 0), lu = (rows + 3) / 4;
-    if constexpr (M >= 3) {
-      if (lu <= 5) return launch_q32<M, 12, 3, 1, false, 5>(a, a.w, a.s, grid, F, st);
-      if (lu == 6) return launch_q32<M, 12, 3, 1, false, 6>(a, a.w, a.s, grid, F, st);
-      if (lu == 7) return launch_q32<M, 12, 3, 1, false, 7>(a, a.w, a.s, grid, F, st);
-    }
-    return launch_q32<M, 12, 3, 1>(a, a.w, a.s, grid, F, st);
-  }
-  if (g.P == 2) return launch_q32<M, 10, 2, 1>(a, a.w, a.s, grid, F, st);
-  if (g.Q == 12) return launch_q32<M, 12, 1, 1>(a, a.w, a.s, grid, F, st);
-  return launch_q32<M, 10, 1, 1>(a, a.w, a.s, grid, F, st);
+  if (g.P == 3) return launch_q32_lu<M, 12, 3>(a, grid, F, st);
+  if (g.P == 2) return launch_q32_lu<M, 10, 2>(a, grid, F, st);
+  if (g.Q == 12) return launch_q32_lu<M, 12, 1>(a, grid, F, st);
+  return launch_q32_lu<M, 10, 1>(a, grid, F, st);
 }
 
 static hipError_t launch_q32_any(const QmmArgs &a, hipStream_t st) {
