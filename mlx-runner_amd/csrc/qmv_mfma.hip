@@ -386,10 +386,14 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
         *(uint2 *)(st + 8 * lane) = make_uint2(sv0[d], sv1[d]);
       else
         *(uint32_t *)(st + 4 * lane) = sv0[d];
-      // unit r + D of this pass, or of the next one (a select, not a division); after
-      // the last pass's last unit the clamped rows of this pass (one row, cached)
+      // unit r + D of this pass, or of the next one (a select, not a division).  After the
+      // last pass's last unit: with one unit in flight nothing, so the wave ends without
+      // waiting on a spare unit's loads; with two the clamped rows of this pass (one row,
+      // cached), since loads under a branch would make the wait for the other buffer
+      // conservative
       const bool wrap = p + 1 < P && r + D >= uppd;
-      load_from(unit_addr(wrap ? p + 1 : p, wrap ? r + D - uppd : r + D), d);
+      if (D > 1 || p + 1 < P || r + D < uppd)
+        load_from(unit_addr(wrap ? p + 1 : p, wrap ? r + D - uppd : r + D), d);
       const bool live = r < upp;
       // a slice past K (last pass only) re-read the last slice: its sums are dropped
       const bool real = P == 1 || p * Q + q < S;
