@@ -773,12 +773,13 @@ __global__ __launch_bounds__(64 * Q) void qmv_deq16_kernel(int N, int K, int M, 
   // a do-while: every workgroup has a row block
   int rb = 0, rbf = 0;  // rbf = rb % F, kept by a counter
   do {
-    // unit rb: registers -> tile, then refill them with unit rb + 1 (past the last: clamped
-    // rows, unused).  One wave's LDS accesses run in order: the reads below see this unit.
+    // unit rb: registers -> tile, then refill them with unit rb + 1 (after the last unit
+    // nothing: the wave ends without waiting on a spare unit's loads).  One wave's LDS
+    // accesses run in order: the reads below see this unit.
 #pragma unroll
     for (int i = 0; i < 4; ++i) *(uint4 *)(wt + (4 * i + (lane >> 4)) * QD_PITCH + 16 * (lane & 15)) = wv[i];
     *(uint2 *)(st + 8 * lane) = sv;
-    load_unit(rb + 1);
+    if (rb + 1 < nrb) load_unit(rb + 1);
     uint4 wq[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) wq[i] = *(const uint4 *)(wt + n * QD_PITCH + 64 * h + 16 * i);
