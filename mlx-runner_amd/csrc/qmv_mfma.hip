@@ -190,7 +190,12 @@ constexpr size_t qf_lds_bytes(int M, int Q, int F) {
 // p Q + q (a slice past K re-reads the last slice and its sums are replaced by
 // zero), re-splits x for it and adds its partial sums to those of earlier
 // passes; the partials of every row block stay in LDS until the last pass.
-template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false>
+//
+// S1 > 0 (nvfp4, one unit in flight, every workgroup two row blocks, the second of at most
+// 4 S1 rows): the row-block loop runs as two unrolled steps, and the second block's units
+// make only their first S1 loads (the rest would re-read the range's last row for output
+// rows that are dropped; their tile rows keep stale bytes, which reach only those rows).
+template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false, int S1 = 0>
 __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, int rbase, int rrem,
                                                           const uint16_t *__restrict__ x,
                                                           const uint8_t *__restrict__ w,
@@ -257,9 +262,12 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
     a.so = (uint32_t)row_of(rb, lane >> 2) * (uint32_t)srow + scol;
     return a;
   };
-  auto load_from = [&](const UnitAddr &a, int buf) __attribute__((always_inline)) {
+  static_assert(S1 == 0 || (MODE == NVFP4 && NMAT == 1 && D == 1 && S1 < G::LOADS), "short row block");
+  using AllLoads = std::integral_constant<int, G::LOADS>;
+  auto load_from = [&](const UnitAddr &a, int buf, auto nl) __attribute__((always_inline)) {
+    constexpr int NL = decltype(nl)::value;
 #pragma unroll
-    for (int i = 0; i < G::LOADS; ++i) wv[buf][i] = load_stream16(wbase(i) + a.wo[i]);
+    for (int i = 0; i < NL; ++i) wv[buf][i] = load_stream16(wbase(i) + a.wo[i]);
     const uint8_t *sp = sbase + a.so;
     if constexpr (MODE == NVFP4) {
       const uint2 t2 = *(const uint2 *)sp;
@@ -270,7 +278,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
       sv1[buf] = 0;
     }
   };
-  load_from(unit_addr(0, 0), 0);
+  load_from(unit_addr(0, 0), 0, AllLoads{});
 
   // 3) x split into records in this wave's tile (before it holds weights), then the
   //    A operands of the slice's 4 chunks into registers, kept for the pass.
@@ -331,7 +339,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
   };
   prep(xr[0]);
 #pragma unroll
-  for (int d = 1; d < D; ++d) load_from(unit_addr(0, d), d);
+  for (int d = 1; d < D; ++d) load_from(unit_addr(0, d), d, AllLoads{});
 
   // sum the waves' partials of row blocks [rb_first, rb_last] in wave order
   auto flush = [&](int rb_first, int rb_last) __attribute__((always_inline)) {
@@ -372,8 +380,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
    // has a row block, and the compiler then counts the next pass's x loads as
    // older than the unit loads (an exact wait before the split, not vmcnt(0)).
    int rbf = 0;  // rb % F, kept by a counter (no division in the loop)
-   int r0 = 0;
-   do {
+   auto units = [&](const int r0) __attribute__((always_inline)) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int r = r0 + d, rb = r;
@@ -381,7 +388,8 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
       // the buffer with unit u + D (past the last unit: clamped rows, unused)
 #pragma unroll
       for (int i = 0; i < G::LOADS; ++i)
-        *(uint4 *)(wt + (RPL * i + lane / LPR) * G::PITCH + 16 * (lane % LPR)) = wv[d][i];
+        if (S1 == 0 || r == 0 || i < S1)
+          *(uint4 *)(wt + (RPL * i + lane / LPR) * G::PITCH + 16 * (lane % LPR)) = wv[d][i];
       if constexpr (MODE == NVFP4)
         *(uint2 *)(st + 8 * lane) = make_uint2(sv0[d], sv1[d]);
       else
@@ -392,8 +400,14 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
       // cached), since loads under a branch would make the wait for the other buffer
       // conservative
       const bool wrap = p + 1 < P && r + D >= uppd;
-      if (D > 1 || p + 1 < P || r + D < uppd)
-        load_from(unit_addr(wrap ? p + 1 : p, wrap ? r + D - uppd : r + D), d);
+      if constexpr (S1 > 0) {  // (r is a constant here: the two steps are unrolled)
+        if (r == 0)
+          load_from(unit_addr(p, 1), d, std::integral_constant<int, (S1 > 0 ? S1 : 1)>{});
+        else if (p + 1 < P)
+          load_from(unit_addr(p + 1, 0), d, AllLoads{});
+      } else if (D > 1 || p + 1 < P || r + D < uppd) {
+        load_from(unit_addr(wrap ? p + 1 : p, wrap ? r + D - uppd : r + D), d, AllLoads{});
+      }
       const bool live = r < upp;
       // a slice past K (last pass only) re-read the last slice: its sums are dropped
       const bool real = P == 1 || p * Q + q < S;
@@ -466,7 +480,15 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
       if (live && p == P - 1 && (rbf + 1 == F || rb + 1 == nrb)) flush(rb - rbf, rb);
       rbf = rbf + 1 == F ? 0 : rbf + 1;
     }
-   } while ((r0 += D) < uppd);
+   };
+   if constexpr (S1 > 0) {
+#pragma unroll
+     for (int r0 = 0; r0 < 2; ++r0) units(r0);
+   } else {
+     int r0 = 0;
+     do units(r0);
+     while ((r0 += D) < uppd);
+   }
   }
 }
 
@@ -906,10 +928,10 @@ bool qmv_mfma_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up)
   return (((uintptr_t)w_up) & 15) == 0 && (((uintptr_t)s_up) & 7) == 0;
 }
 
-template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false>
+template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false, int S1 = 0>
 static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
                             hipStream_t st) {
-  auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D, P, PARTS>;
+  auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D, P, PARTS, S1>;
   const size_t lds = qf_lds_bytes<MODE>(M, Q, F);
   static std::atomic<uint64_t> lds_set{0};
   const hipError_t e = ensure_dynamic_lds(lds_set, (const void *)kern, 160 * 1024);
@@ -930,6 +952,18 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
   if constexpr (NMAT == 1 && !PARTS) {
     const QfShape g = qf_shape(a.K);
     if (g.P == 3) {
+      if constexpr (MODE == NVFP4 && M == 2) {
+        // 17-28 rows per workgroup (the down projection, 5120 rows: 20): two row blocks,
+        // the second's units make only the loads of its rows (x of 2 rows: 12.71 -> 11.89 us
+        // at 5120 x 17408; at one row 10.89 -> 11.0, not used there)
+        const int rmin = a.N / grid, rmax = rmin + (a.N % grid ? 1 : 0);
+        if (rmin > 16 && rmax <= 28) {
+          const int s1 = (rmax - 16 + 3) / 4;
+          if (s1 == 1) return launch_qf<MODE, M, 12, 1, 1, 3, false, 1>(a, w2, s2, grid, F, st);
+          if (s1 == 2) return launch_qf<MODE, M, 12, 1, 1, 3, false, 2>(a, w2, s2, grid, F, st);
+          return launch_qf<MODE, M, 12, 1, 1, 3, false, 3>(a, w2, s2, grid, F, st);
+        }
+      }
       if constexpr (M <= 5) return launch_qf<MODE, M, 12, 1, 1, 3>(a, w2, s2, grid, F, st);
       return hipErrorInvalidValue;  // (qmv_mfma_ok: x of three passes would not fit in registers)
     }
