@@ -191,10 +191,11 @@ constexpr size_t qf_lds_bytes(int M, int Q, int F) {
 // zero), re-splits x for it and adds its partial sums to those of earlier
 // passes; the partials of every row block stay in LDS until the last pass.
 //
-// S1 > 0 (nvfp4, one unit in flight, every workgroup two row blocks, the second of at most
-// 4 S1 rows): the row-block loop runs as two unrolled steps, and the second block's units
-// make only their first S1 loads (the rest would re-read the range's last row for output
-// rows that are dropped; their tile rows keep stale bytes, which reach only those rows).
+// S1 > 0 (one unit in flight, every workgroup two row blocks, the second of at most S1
+// loads' rows: 4 per load in nvfp4, 2 in mxfp8): the row-block loop runs as two unrolled
+// steps, and the second block's units make only their first S1 loads (the rest would
+// re-read the range's last row for output rows that are dropped; their tile rows keep
+// stale bytes, which reach only those rows).
 template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false, int S1 = 0>
 __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, int rbase, int rrem,
                                                           const uint16_t *__restrict__ x,
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
     a.so = (uint32_t)row_of(rb, lane >> 2) * (uint32_t)srow + scol;
     return a;
   };
-  static_assert(S1 == 0 || (MODE == NVFP4 && NMAT == 1 && D == 1 && S1 < G::LOADS), "short row block");
+  static_assert(S1 == 0 || (NMAT == 1 && D == 1 && S1 < G::LOADS), "short row block");
   using AllLoads = std::integral_constant<int, G::LOADS>;
   auto load_from = [&](const UnitAddr &a, int buf, auto nl) __attribute__((always_inline)) {
     constexpr int NL = decltype(nl)::value;
@@ -380,10 +381,15 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
    // has a row block, and the compiler then counts the next pass's x loads as
    // older than the unit loads (an exact wait before the split, not vmcnt(0)).
    int rbf = 0;  // rb % F, kept by a counter (no division in the loop)
-   auto units = [&](const int r0) __attribute__((always_inline)) {
+   int r0 = 0;
+   // (S1 > 0: the two row blocks as two unrolled steps of one do-while pass each, so that
+   // r is a constant in each and so are its loads; otherwise one step, the loop as is)
+#pragma unroll
+   for (int step = 0; step < (S1 > 0 ? 2 : 1); ++step) {
+   do {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      const int r = r0 + d, rb = r;
+      const int r = (S1 > 0 ? step : r0) + d, rb = r;
       // unit u: registers -> tile (the x records are no longer needed there), then refill
       // the buffer with unit u + D (past the last unit: clamped rows, unused)
 #pragma unroll
@@ -400,7 +406,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
       // cached), since loads under a branch would make the wait for the other buffer
       // conservative
       const bool wrap = p + 1 < P && r + D >= uppd;
-      if constexpr (S1 > 0) {  // (r is a constant here: the two steps are unrolled)
+      if constexpr (S1 > 0) {  // (D = 1 and two row blocks: step r is 0 or 1)
         if (r == 0)
           load_from(unit_addr(p, 1), d, std::integral_constant<int, (S1 > 0 ? S1 : 1)>{});
         else if (p + 1 < P)
@@ -480,14 +486,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
       if (live && p == P - 1 && (rbf + 1 == F || rb + 1 == nrb)) flush(rb - rbf, rb);
       rbf = rbf + 1 == F ? 0 : rbf + 1;
     }
-   };
-   if constexpr (S1 > 0) {
-#pragma unroll
-     for (int r0 = 0; r0 < 2; ++r0) units(r0);
-   } else {
-     int r0 = 0;
-     do units(r0);
-     while ((r0 += D) < uppd);
+   } while (S1 == 0 && (r0 += D) < uppd);
    }
   }
 }
@@ -951,19 +950,15 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
                               hipStream_t st) {
   if constexpr (NMAT == 1 && !PARTS) {
     const QfShape g = qf_shape(a.K);
+    // 17-20 rows per workgroup (5120 rows: the down projection, o_proj, out_proj): two row
+    // blocks, the second's units make only the loads of its 4 rows (nvfp4 x of 2 rows at
+    // 5120 x 17408: 12.71 -> 11.89 us; at one row 10.89 -> 11.0, not used there)
+    const int rmin = a.N / grid, rmax = rmin + (a.N % grid ? 1 : 0);
+    const bool short2 = rmin > 16 && rmax <= 20 && (MODE == MXFP8 || M == 2);
+    constexpr int S1 = MODE == NVFP4 ? 1 : 2;
     if (g.P == 3) {
-      if constexpr (MODE == NVFP4 && M == 2) {
-        // 17-28 rows per workgroup (the down projection, 5120 rows: 20): two row blocks,
-        // the second's units make only the loads of its rows (x of 2 rows: 12.71 -> 11.89 us
-        // at 5120 x 17408; at one row 10.89 -> 11.0, not used there)
-        const int rmin = a.N / grid, rmax = rmin + (a.N % grid ? 1 : 0);
-        if (rmin > 16 && rmax <= 28) {
-          const int s1 = (rmax - 16 + 3) / 4;
-          if (s1 == 1) return launch_qf<MODE, M, 12, 1, 1, 3, false, 1>(a, w2, s2, grid, F, st);
-          if (s1 == 2) return launch_qf<MODE, M, 12, 1, 1, 3, false, 2>(a, w2, s2, grid, F, st);
-          return launch_qf<MODE, M, 12, 1, 1, 3, false, 3>(a, w2, s2, grid, F, st);
-        }
-      }
+      if constexpr (M <= 5)
+        if (short2) return launch_qf<MODE, M, 12, 1, 1, 3, false, S1>(a, w2, s2, grid, F, st);
       if constexpr (M <= 5) return launch_qf<MODE, M, 12, 1, 1, 3>(a, w2, s2, grid, F, st);
       return hipErrorInvalidValue;  // (qmv_mfma_ok: x of three passes would not fit in registers)
     }
@@ -971,7 +966,10 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
       if constexpr (M <= 8) return launch_qf<MODE, M, 10, 1, 1, 2>(a, w2, s2, grid, F, st);
       return hipErrorInvalidValue;
     }
-    if (g.Q == 12) return launch_qf<MODE, M, 12, 1, 1, 1>(a, w2, s2, grid, F, st);
+    if (g.Q == 12) {
+      if (short2) return launch_qf<MODE, M, 12, 1, 1, 1, false, S1>(a, w2, s2, grid, F, st);
+      return launch_qf<MODE, M, 12, 1, 1, 1>(a, w2, s2, grid, F, st);
+    }
   }
   // (the MLP form and the grouped form at nvfp4 M = 2 would spill with two units in flight)
   // (nor x of 9-16 rows, whose x and A operands take twice the registers)
