@@ -652,9 +652,14 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
       for (int li = 0; li < LU; ++li) *(uint4 *)(wt + (4 * li + (lane >> 4)) * Q32_PITCH + 16 * (lane & 15)) = wv[li];
       *(uint4 *)(st + 16 * lane) = sv;
       // the next unit: this pass's next row block or the next pass's first; after the
-      // last pass's last unit the clamped rows past the range (one row, cached)
+      // last pass's last unit the clamped rows past the range (one row, cached), except
+      // with one row block and one pass (dropped there: faster at K = 5120 / 6144, slower
+      // with several passes)
       const bool wrap = p + 1 < P && rb + 1 >= nrb;
-      load_unit(wrap ? p + 1 : p, wrap ? 0 : rb + 1);
+      if constexpr (LU < 8 && P == 1) {  // one row block and one pass: no next unit
+      } else {
+        load_unit(wrap ? p + 1 : p, wrap ? 0 : rb + 1);
+      }
       float acc[M];
 #pragma unroll
       for (int m = 0; m < M; ++m) acc[m] = 0.f;
