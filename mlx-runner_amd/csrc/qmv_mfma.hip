@@ -196,7 +196,11 @@ constexpr size_t qf_lds_bytes(int M, int Q, int F) {
 // steps, and the second block's units make only their first S1 loads (the rest would
 // re-read the range's last row for output rows that are dropped; their tile rows keep
 // stale bytes, which reach only those rows).
-template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false, int S1 = 0>
+//
+// SL > 0 (nvfp4, one unit in flight, one pass, every workgroup the same 3 or more row
+// blocks, the last of at most 4 SL rows per matrix): likewise for the last row block, with
+// the loop's last two steps unrolled after it.
+template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false, int S1 = 0, int SL = 0>
 __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, int rbase, int rrem,
                                                           const uint16_t *__restrict__ x,
                                                           const uint8_t *__restrict__ w,
@@ -264,11 +268,16 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
     return a;
   };
   static_assert(S1 == 0 || (NMAT == 1 && D == 1 && S1 < G::LOADS), "short row block");
+  static_assert(SL == 0 || (MODE == NVFP4 && D == 1 && P == 1 && !PARTS && S1 == 0 && SL < G::LOADS / NMAT),
+                "short last row block");
+  // load i of a unit whose rows are at most NL loads' worth per matrix (NL = G::LOADS: all)
+  auto load_on = [](int i, int nl) { return (NMAT == 2 ? i % (G::LOADS / 2) : i) < nl; };
   using AllLoads = std::integral_constant<int, G::LOADS>;
   auto load_from = [&](const UnitAddr &a, int buf, auto nl) __attribute__((always_inline)) {
     constexpr int NL = decltype(nl)::value;
 #pragma unroll
-    for (int i = 0; i < NL; ++i) wv[buf][i] = load_stream16(wbase(i) + a.wo[i]);
+    for (int i = 0; i < G::LOADS; ++i)
+      if (load_on(i, NL)) wv[buf][i] = load_stream16(wbase(i) + a.wo[i]);
     const uint8_t *sp = sbase + a.so;
     if constexpr (MODE == NVFP4) {
       const uint2 t2 = *(const uint2 *)sp;
@@ -383,18 +392,19 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
    int rbf = 0;  // rb % F, kept by a counter (no division in the loop)
    int r0 = 0;
    // (S1 > 0: the two row blocks as two unrolled steps of one do-while pass each, so that
-   // r is a constant in each and so are its loads; otherwise one step, the loop as is)
+   // r is a constant in each and so are its loads; SL > 0: the loop over all but the last
+   // two row blocks, then those two as unrolled steps; otherwise one step, the loop as is)
 #pragma unroll
-   for (int step = 0; step < (S1 > 0 ? 2 : 1); ++step) {
+   for (int step = 0; step < (S1 > 0 ? 2 : SL > 0 ? 3 : 1); ++step) {
    do {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      const int r = (S1 > 0 ? step : r0) + d, rb = r;
+      const int r = (S1 > 0 ? step : SL > 0 && step > 0 ? nrb - 3 + step : r0) + d, rb = r;
       // unit u: registers -> tile (the x records are no longer needed there), then refill
       // the buffer with unit u + D (past the last unit: clamped rows, unused)
 #pragma unroll
       for (int i = 0; i < G::LOADS; ++i)
-        if (S1 == 0 || r == 0 || i < S1)
+        if ((S1 == 0 || r == 0 || i < S1) && (SL == 0 || step < 2 || load_on(i, SL)))
           *(uint4 *)(wt + (RPL * i + lane / LPR) * G::PITCH + 16 * (lane % LPR)) = wv[d][i];
       if constexpr (MODE == NVFP4)
         *(uint2 *)(st + 8 * lane) = make_uint2(sv0[d], sv1[d]);
@@ -411,6 +421,11 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
           load_from(unit_addr(p, 1), d, std::integral_constant<int, (S1 > 0 ? S1 : 1)>{});
         else if (p + 1 < P)
           load_from(unit_addr(p + 1, 0), d, AllLoads{});
+      } else if constexpr (SL > 0) {  // (D = 1, one pass; step 2 is the last unit)
+        if (step == 0)
+          load_from(unit_addr(p, r + 1), d, AllLoads{});
+        else if (step == 1)
+          load_from(unit_addr(p, r + 1), d, std::integral_constant<int, (SL > 0 ? SL : 1)>{});
       } else if (D > 1 || p + 1 < P || r + D < uppd) {
         load_from(unit_addr(wrap ? p + 1 : p, wrap ? r + D - uppd : r + D), d, AllLoads{});
       }
@@ -486,7 +501,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
       if (live && p == P - 1 && (rbf + 1 == F || rb + 1 == nrb)) flush(rb - rbf, rb);
       rbf = rbf + 1 == F ? 0 : rbf + 1;
     }
-   } while (S1 == 0 && (r0 += D) < uppd);
+   } while (S1 == 0 && (SL > 0 ? step == 0 && ++r0 < nrb - 2 : (r0 += D) < uppd));
    }
   }
 }
@@ -932,10 +947,10 @@ bool qmv_mfma_mlp_ok(const QmmArgs &a, const uint8_t *w_up, const uint8_t *s_up)
   return (((uintptr_t)w_up) & 15) == 0 && (((uintptr_t)s_up) & 7) == 0;
 }
 
-template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false, int S1 = 0>
+template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false, int S1 = 0, int SL = 0>
 static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
                             hipStream_t st) {
-  auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D, P, PARTS, S1>;
+  auto kern = qmv_mfma_kernel<MODE, M, Q, NMAT, D, P, PARTS, S1, SL>;
   const size_t lds = qf_lds_bytes<MODE>(M, Q, F);
   static std::atomic<uint64_t> lds_set{0};
   const hipError_t e = ensure_dynamic_lds(lds_set, (const void *)kern, 160 * 1024);
@@ -943,6 +958,16 @@ static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * Q), lds, st, a.N, a.K, F, a.N / grid, a.N % grid,
                      (const uint16_t *)a.x, a.w, a.s, w2, s2, yout_of(a));
   return hipGetLastError();
+}
+
+// nvfp4 loads (4 rows each, per matrix) of the last row block of RB-row blocks when every
+// workgroup has the same 3 or more row blocks and the last is short; 0 otherwise.
+static int qf_short_last(const QmmArgs &a, int grid, int RB) {
+  const int rmin = a.N / grid, rmax = rmin + (a.N % grid ? 1 : 0);
+  const int nb = (rmax + RB - 1) / RB;
+  if (nb < 3 || (rmin + RB - 1) / RB != nb) return 0;
+  const int sl = (rmax - RB * (nb - 1) + 3) / 4;
+  return sl < RB / 4 ? sl : 0;
 }
 
 // Two units in flight per wave when each workgroup has few row blocks (the call
@@ -973,6 +998,14 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
     }
     if (g.Q == 12) {
       if (short2) return launch_qf<MODE, M, 12, 1, 1, 1, false, S1>(a, w2, s2, grid, F, st);
+      if constexpr (MODE == NVFP4) {
+        switch (qf_short_last(a, grid, 16)) {
+          case 1: return launch_qf<MODE, M, 12, 1, 1, 1, false, 0, 1>(a, w2, s2, grid, F, st);
+          case 2: return launch_qf<MODE, M, 12, 1, 1, 1, false, 0, 2>(a, w2, s2, grid, F, st);
+          case 3: return launch_qf<MODE, M, 12, 1, 1, 1, false, 0, 3>(a, w2, s2, grid, F, st);
+          default: break;
+        }
+      }
       return launch_qf<MODE, M, 12, 1, 1, 1>(a, w2, s2, grid, F, st);
     }
   }
@@ -980,6 +1013,16 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
   // (nor x of 9-16 rows, whose x and A operands take twice the registers)
   if constexpr (!((NMAT == 2 || PARTS) && MODE == NVFP4 && M == 2) && M <= 8)
     if (nrb <= 4) return launch_qf<MODE, M, 10, NMAT, 2, 1, PARTS>(a, w2, s2, grid, F, st);
+  if constexpr (MODE == NVFP4 && !PARTS) {
+    const int sl = qf_short_last(a, grid, NMAT == 2 ? 8 : 16);
+    if constexpr (NMAT == 1) {
+      if (sl == 1) return launch_qf<MODE, M, 10, NMAT, 1, 1, false, 0, 1>(a, w2, s2, grid, F, st);
+      if (sl == 2) return launch_qf<MODE, M, 10, NMAT, 1, 1, false, 0, 2>(a, w2, s2, grid, F, st);
+      if (sl == 3) return launch_qf<MODE, M, 10, NMAT, 1, 1, false, 0, 3>(a, w2, s2, grid, F, st);
+    } else {
+      if (sl == 1) return launch_qf<MODE, M, 10, NMAT, 1, 1, false, 0, 1>(a, w2, s2, grid, F, st);
+    }
+  }
   return launch_qf<MODE, M, 10, NMAT, 1, 1, PARTS>(a, w2, s2, grid, F, st);
 }
 
