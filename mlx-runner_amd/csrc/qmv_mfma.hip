@@ -536,7 +536,11 @@ constexpr size_t q32_lds_bytes(int M, int Q, int F) { return (size_t)Q * Q32_WAV
 // LU < 8 (one row block per workgroup, at most 4 LU rows): the unit's loads of rows past
 // the range, which every unit would make and whose sums are dropped, are not made (tile
 // rows 4 LU .. 31 keep stale bytes, which reach only the dropped output rows).
-template <int M, int Q, int P, int NMAT, bool PARTS = false, int LU = 8>
+//
+// SL > 0 (one pass, every workgroup the same 2 or more row blocks, the last of at most 4 SL
+// rows per matrix): the last row block's units make only the loads of its rows, and none
+// follows the last unit; the loop's last two steps run unrolled after it.
+template <int M, int Q, int P, int NMAT, bool PARTS = false, int LU = 8, int SL = 0>
 __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F, int rbase, int rrem,
                                                             const uint16_t *__restrict__ x,
                                                             const uint8_t *__restrict__ w,
@@ -577,10 +581,14 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
   // W and scale addresses are 32-bit offsets (the host checks that a matrix is under 4 GiB).
   const uint8_t *sbase = NMAT == 2 && lane >= 32 ? s2 : s;  // this lane's scale rows
   static_assert(LU == 8 || (NMAT == 1 && LU >= 1 && LU < 8), "rows per unit");
-  auto load_unit = [&](int pass, int rb) __attribute__((always_inline)) {
+  static_assert(SL == 0 || (P == 1 && LU == 8 && SL < 8 / NMAT), "short last row block");
+  // load i of a unit of at most nl loads' rows per matrix
+  auto load_on = [](int i, int nl) { return (NMAT == 2 ? i & 3 : i) < nl; };
+  auto load_unit = [&](int pass, int rb, int nl = 8) __attribute__((always_inline)) {
     const int sl = slice_of(pass);
 #pragma unroll
     for (int i = 0; i < LU; ++i) {
+      if (!load_on(i, nl)) continue;
       const uint8_t *wm = NMAT == 2 && i >= 4 ? w2 : w;  // a load's rows are all in one matrix
       wv[i] = load_stream16(wm + ((uint32_t)row_of(rb, 4 * i + (lane >> 4)) * (uint32_t)wrow + sl * 256 +
                                   16 * (lane & 15)));
@@ -660,18 +668,29 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
     // a do-while: every workgroup has a row block, and the compiler then counts the
     // next pass's x loads as older than the unit loads (exact wait before the split)
     int rb = 0, rbf = 0;  // rbf = rb % F, kept by a counter (no division in the loop)
+    // (SL > 0: the units before the last two, then those two as unrolled steps)
+#pragma unroll
+    for (int step = 0; step < (SL > 0 ? 3 : 1); ++step) {
     do {
+      if (SL > 0 && step == 0 && rb >= nrb - 2) break;
       // unit (p, rb): registers -> tile (the x records are no longer needed there), then
       // refill the registers with the next unit (past the last one: clamped, unused)
 #pragma unroll
-      for (int li = 0; li < LU; ++li) *(uint4 *)(wt + (4 * li + (lane >> 4)) * Q32_PITCH + 16 * (lane & 15)) = wv[li];
+      for (int li = 0; li < LU; ++li)
+        if (SL == 0 || step < 2 || load_on(li, SL))
+          *(uint4 *)(wt + (4 * li + (lane >> 4)) * Q32_PITCH + 16 * (lane & 15)) = wv[li];
       *(uint4 *)(st + 16 * lane) = sv;
       // the next unit: this pass's next row block or the next pass's first; after the
       // last pass's last unit the clamped rows past the range (one row, cached), except
       // with one row block and one pass (dropped there: faster at K = 5120 / 6144, slower
       // with several passes)
       const bool wrap = p + 1 < P && rb + 1 >= nrb;
-      if constexpr (LU < 8 && P == 1) {  // one row block and one pass: no next unit
+      if constexpr (SL > 0) {  // the next unit: full, or the short last one, or none
+        if (step == 0)
+          load_unit(p, rb + 1);
+        else if (step == 1)
+          load_unit(p, rb + 1, SL);
+      } else if constexpr (LU < 8 && P == 1) {  // one row block and one pass: no next unit
       } else {
         load_unit(wrap ? p + 1 : p, wrap ? 0 : rb + 1);
       }
@@ -722,7 +741,8 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma32_kernel(int N, int K, int F,
       // with several passes the host sets F >= nrb: one flush, after the last pass
       if (p == P - 1 && (rbf + 1 == F || rb + 1 == nrb)) flush(rb - rbf, rb);
       rbf = rbf + 1 == F ? 0 : rbf + 1;
-    } while (++rb < nrb);
+    } while (SL > 0 ? (step == 0 ? ++rb < nrb - 2 : (++rb, false)) : ++rb < nrb);
+    }
   }
 }
 
@@ -961,11 +981,11 @@ static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *
 }
 
 // nvfp4 loads (4 rows each, per matrix) of the last row block of RB-row blocks when every
-// workgroup has the same 3 or more row blocks and the last is short; 0 otherwise.
-static int qf_short_last(const QmmArgs &a, int grid, int RB) {
+// workgroup has the same min_nb or more row blocks and the last is short; 0 otherwise.
+static int qf_short_last(const QmmArgs &a, int grid, int RB, int min_nb = 3) {
   const int rmin = a.N / grid, rmax = rmin + (a.N % grid ? 1 : 0);
   const int nb = (rmax + RB - 1) / RB;
-  if (nb < 3 || (rmin + RB - 1) / RB != nb) return 0;
+  if (nb < min_nb || (rmin + RB - 1) / RB != nb) return 0;
   const int sl = (rmax - RB * (nb - 1) + 3) / 4;
   return sl < RB / 4 ? sl : 0;
 }
@@ -1065,10 +1085,10 @@ static hipError_t launch_qf_any(const QmmArgs &a, const uint8_t *w2, const uint8
 }
 
 // nvfp4 on the 32x32x64 form: 32-row blocks, one unit in flight per wave.
-template <int M, int Q, int P, int NMAT, bool PARTS = false, int LU = 8>
+template <int M, int Q, int P, int NMAT, bool PARTS = false, int LU = 8, int SL = 0>
 static hipError_t launch_q32(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F,
                              hipStream_t st) {
-  auto kern = qmv_mfma32_kernel<M, Q, P, NMAT, PARTS, LU>;
+  auto kern = qmv_mfma32_kernel<M, Q, P, NMAT, PARTS, LU, SL>;
   static std::atomic<uint64_t> lds_set{0};
   const hipError_t e = ensure_dynamic_lds(lds_set, (const void *)kern, 160 * 1024);
   if (e != hipSuccess) return e;
@@ -1111,6 +1131,18 @@ static hipError_t launch_q32_lu(const QmmArgs &a, int grid, int F, hipStream_t s
     if (lu <= 5) return launch_q32<M, Q, P, 1, false, 5>(a, a.w, a.s, grid, F, st);
     if (lu == 6) return launch_q32<M, Q, P, 1, false, 6>(a, a.w, a.s, grid, F, st);
     if (lu == 7) return launch_q32<M, Q, P, 1, false, 7>(a, a.w, a.s, grid, F, st);
+  }
+  if constexpr (P == 1 && M >= 3) {  // a short last row block of 2 or more
+    switch (qf_short_last(a, grid, 32, 2)) {
+      case 1: return launch_q32<M, Q, P, 1, false, 8, 1>(a, a.w, a.s, grid, F, st);
+      case 2: return launch_q32<M, Q, P, 1, false, 8, 2>(a, a.w, a.s, grid, F, st);
+      case 3: return launch_q32<M, Q, P, 1, false, 8, 3>(a, a.w, a.s, grid, F, st);
+      case 4: return launch_q32<M, Q, P, 1, false, 8, 4>(a, a.w, a.s, grid, F, st);
+      case 5: return launch_q32<M, Q, P, 1, false, 8, 5>(a, a.w, a.s, grid, F, st);
+      case 6: return launch_q32<M, Q, P, 1, false, 8, 6>(a, a.w, a.s, grid, F, st);
+      case 7: return launch_q32<M, Q, P, 1, false, 8, 7>(a, a.w, a.s, grid, F, st);
+      default: break;
+    }
   }
   return launch_q32<M, Q, P, 1>(a, a.w, a.s, grid, F, st);
 }
@@ -1157,6 +1189,15 @@ static hipError_t launch_q32_mlp(const QmmArgs &a, const uint8_t *w_up, const ui
   const int grid = rbs < cus ? rbs : cus;
   const int nrb = q32_nrb(a, cus, 2);
   const int F = q32_flush_rows(a, nrb);
+  switch (qf_short_last(a, grid, 16, 2)) {  // a short last row block of 2 or more
+    case 1: return a.M == 3 ? launch_q32<3, 10, 1, 2, false, 8, 1>(a, w_up, s_up, grid, F, st)
+                            : launch_q32<4, 10, 1, 2, false, 8, 1>(a, w_up, s_up, grid, F, st);
+    case 2: return a.M == 3 ? launch_q32<3, 10, 1, 2, false, 8, 2>(a, w_up, s_up, grid, F, st)
+                            : launch_q32<4, 10, 1, 2, false, 8, 2>(a, w_up, s_up, grid, F, st);
+    case 3: return a.M == 3 ? launch_q32<3, 10, 1, 2, false, 8, 3>(a, w_up, s_up, grid, F, st)
+                            : launch_q32<4, 10, 1, 2, false, 8, 3>(a, w_up, s_up, grid, F, st);
+    default: break;
+  }
   if (a.M == 3) return launch_q32<3, 10, 1, 2>(a, w_up, s_up, grid, F, st);
   return launch_q32<4, 10, 1, 2>(a, w_up, s_up, grid, F, st);
 }
