@@ -395,7 +395,9 @@ def make_x(rng, M, K, kind):
 # mxfp8 M = 5-8 the 16x16x128 form with all 16 A columns (8 rows x hi|lo) live, M = 9-16
 # with two A operands per chunk (their records made 8 rows at a time); nvfp4 M = 5-8 the
 # dequantizing kernel (W -> bf16, all 16 x rows on the bf16 MFMA), as nvfp4 M = 9-16, down
-# to N = 100 (7 workgroups of 14-15 rows).
+# to N = 100 (7 workgroups of 14-15 rows).  N = 17408 (68 rows per workgroup), 10240 (40)
+# and 12288 (48) end every workgroup's range with a short row block, whose units load only
+# its rows.
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 1, 70001), ("nvfp4", 2, 4099),
                                       ("nvfp4", 2, 16384), ("nvfp4", 3, 4099), ("nvfp4", 3, 70001),
                                       ("nvfp4", 4, 16400), ("mxfp8", 2, 4101), ("mxfp8", 3, 8192),
@@ -404,7 +406,9 @@ def make_x(rng, M, K, kind):
                                       ("mxfp8", 9, 4101), ("mxfp8", 12, 8192), ("mxfp8", 15, 4096),
                                       ("mxfp8", 16, 70001), ("nvfp4", 5, 4099), ("nvfp4", 6, 70001),
                                       ("nvfp4", 7, 5120), ("nvfp4", 8, 16400), ("nvfp4", 9, 4099),
-                                      ("nvfp4", 12, 70001), ("nvfp4", 16, 16400), ("nvfp4", 13, 100)])
+                                      ("nvfp4", 12, 70001), ("nvfp4", 16, 16400), ("nvfp4", 13, 100),
+                                      ("nvfp4", 1, 17408), ("nvfp4", 2, 17408), ("nvfp4", 3, 17408),
+                                      ("nvfp4", 3, 10240), ("nvfp4", 4, 12288)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
 def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
     K = 5120
@@ -473,10 +477,12 @@ def test_decode_mfma_other_k_match_oracle(K, mode, M, N, xkind):
 
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 2, 4099), ("nvfp4", 3, 4099),
                                       ("nvfp4", 4, 16400), ("mxfp8", 3, 4101), ("mxfp8", 4, 70001),
-                                      ("mxfp8", 6, 4101), ("nvfp4", 5, 4099)])
+                                      ("mxfp8", 6, 4101), ("nvfp4", 5, 4099), ("nvfp4", 1, 17408),
+                                      ("nvfp4", 2, 17408), ("nvfp4", 3, 17408), ("nvfp4", 4, 17408)])
 def test_mlp_gate_up_silu_mfma_shapes(mode, M, N):
     """The fused MLP on the MFMA path: equal to two quantized_matmul + silu_mul bit for
-    bit, and within tolerance of the oracle's chain on a row sample."""
+    bit, and within tolerance of the oracle's chain on a row sample.  At N = 17408 (the
+    model's MLP: 68 rows per workgroup) each range ends in a short row block."""
     K = 5120
     rng = np.random.default_rng(N + 7 * M)
     wg, sg = rand_packed(rng, mode, N, K)
