@@ -1031,6 +1031,17 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
   }
   // (the MLP form and the grouped form at nvfp4 M = 2 would spill with two units in flight)
   // (nor x of 9-16 rows, whose x and A operands take twice the registers)
+  // K = 5120, two row blocks of which the second has 4 or 8 rows (5120 rows: 20, 6144: 24):
+  // one unit in flight with the short second block instead of two units in flight (mxfp8
+  // 5120 x 5120: 7.80 -> 6.70 us at M = 2, 8.42 -> 7.30 at M = 4)
+  if constexpr (NMAT == 1 && !PARTS && M <= 8 && (MODE == MXFP8 ? M >= 2 : M == 2)) {
+    const int rmin = a.N / grid, rmax = rmin + (a.N % grid ? 1 : 0);
+    constexpr int RPL = MODE == NVFP4 ? 4 : 2;  // rows per load
+    if (rmin > 16 && (rmax == 20 || rmax == 24)) {
+      if (rmax == 20) return launch_qf<MODE, M, 10, 1, 1, 1, false, 4 / RPL>(a, w2, s2, grid, F, st);
+      return launch_qf<MODE, M, 10, 1, 1, 1, false, 8 / RPL>(a, w2, s2, grid, F, st);
+    }
+  }
   if constexpr (!((NMAT == 2 || PARTS) && MODE == NVFP4 && M == 2) && M <= 8)
     if (nrb <= 4) return launch_qf<MODE, M, 10, NMAT, 2, 1, PARTS>(a, w2, s2, grid, F, st);
   if constexpr (MODE == NVFP4 && !PARTS) {

@@ -397,7 +397,7 @@ def make_x(rng, M, K, kind):
 # dequantizing kernel (W -> bf16, all 16 x rows on the bf16 MFMA), as nvfp4 M = 9-16, down
 # to N = 100 (7 workgroups of 14-15 rows).  N = 17408 (68 rows per workgroup), 10240 (40)
 # and 12288 (48) end every workgroup's range with a short row block, whose units load only
-# its rows.
+# its rows; so do N = 5120 (20) and 6144 (24) with two row blocks, the second short.
 @pytest.mark.parametrize("mode,M,N", [("nvfp4", 1, 16400), ("nvfp4", 1, 70001), ("nvfp4", 2, 4099),
                                       ("nvfp4", 2, 16384), ("nvfp4", 3, 4099), ("nvfp4", 3, 70001),
                                       ("nvfp4", 4, 16400), ("mxfp8", 2, 4101), ("mxfp8", 3, 8192),
@@ -408,7 +408,9 @@ def make_x(rng, M, K, kind):
                                       ("nvfp4", 7, 5120), ("nvfp4", 8, 16400), ("nvfp4", 9, 4099),
                                       ("nvfp4", 12, 70001), ("nvfp4", 16, 16400), ("nvfp4", 13, 100),
                                       ("nvfp4", 1, 17408), ("nvfp4", 2, 17408), ("nvfp4", 3, 17408),
-                                      ("nvfp4", 3, 10240), ("nvfp4", 4, 12288)])
+                                      ("nvfp4", 3, 10240), ("nvfp4", 4, 12288), ("nvfp4", 2, 5120),
+                                      ("nvfp4", 2, 6144), ("mxfp8", 2, 5120), ("mxfp8", 4, 6144),
+                                      ("mxfp8", 8, 5120)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
 def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
     K = 5120
