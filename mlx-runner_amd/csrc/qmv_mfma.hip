@@ -990,10 +990,10 @@ static int qf_short_last(const QmmArgs &a, int grid, int RB, int min_nb = 3) {
   return sl < RB / 4 ? sl : 0;
 }
 
-// Two units in flight per wave when each workgroup has few row blocks (the call
-// is then a few memory latencies long); one otherwise, which streams faster.
-// K = 17408 (three passes, no MLP form) keeps one unit in flight: x of all
-// passes is held in registers.
+// One unit in flight per wave at every size.  (Two, once the rule for ranges of 1-4 row
+// blocks, measured slower on the current kernels at every such shape: nvfp4 M = 2 at
+// 4096 / 12288 x 5120 6.19 -> 4.79 / 9.71 -> 7.41 us with one; the second unit of a
+// one-block range was a clamped re-read.)
 // (grouped calls, PARTS, and the MLP form run K = 5120 only)
 template <int MODE, int M, int NMAT, bool PARTS = false>
 static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t *s2, int grid, int F, int nrb,
@@ -1032,8 +1032,8 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
   // (the MLP form and the grouped form at nvfp4 M = 2 would spill with two units in flight)
   // (nor x of 9-16 rows, whose x and A operands take twice the registers)
   // K = 5120, two row blocks of which the second has 4 or 8 rows (5120 rows: 20, 6144: 24):
-  // one unit in flight with the short second block instead of two units in flight (mxfp8
-  // 5120 x 5120: 7.80 -> 6.70 us at M = 2, 8.42 -> 7.30 at M = 4)
+  // the short second block (mxfp8 5120 x 5120: 7.80 -> 6.70 us at M = 2, 8.42 -> 7.30 at
+  // M = 4, against two units in flight)
   if constexpr (NMAT == 1 && !PARTS && M <= 8 && (MODE == MXFP8 ? M >= 2 : M == 2)) {
     const int rmin = a.N / grid, rmax = rmin + (a.N % grid ? 1 : 0);
     constexpr int RPL = MODE == NVFP4 ? 4 : 2;  // rows per load
@@ -1042,8 +1042,6 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
       return launch_qf<MODE, M, 10, 1, 1, 1, false, 8 / RPL>(a, w2, s2, grid, F, st);
     }
   }
-  if constexpr (!((NMAT == 2 || PARTS) && MODE == NVFP4 && M == 2) && M <= 8)
-    if (nrb <= 4) return launch_qf<MODE, M, 10, NMAT, 2, 1, PARTS>(a, w2, s2, grid, F, st);
   if constexpr (MODE == NVFP4 && !PARTS) {
     const int sl = qf_short_last(a, grid, NMAT == 2 ? 8 : 16);
     if constexpr (NMAT == 1) {
