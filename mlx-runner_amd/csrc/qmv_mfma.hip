@@ -937,16 +937,15 @@ bool qmv_mfma_ok(const QmmArgs &a) {
   // x of every pass is held in registers: 6-8 rows fit two passes, 9-16 rows one
   if ((a.M > 5 && g.P == 3) || (a.M > 8 && g.P > 1)) return false;
   // Where this path is faster than the unpacking GEMV (measured on the 256-CU
-  // MI355X): at M = 1 only for nvfp4, with many rows per CU at K = 5120 (it pays
-  // a per-workgroup x split and pipeline fill) and at K = 17408 (N = 5120: 11.8
-  // against 12.4 us); mxfp8 at M = 1 decodes at 1 VALU op per weight byte and
-  // streams faster through the unpacking GEMV (K = 17408: 17.2 against 19.8 us).
+  // MI355X): nvfp4 at M = 1 with many rows per CU at K = 5120 (it pays a per-workgroup
+  // x split and pipeline fill) and at K = 17408 (N = 5120: 11.8 against 12.4 us).
   // At M >= 2 from N = 4096.
   if (a.M == 1 && a.mode == NVFP4 && g.P == 1 && a.N < 16384) return false;
-  // mxfp8 at M = 1: the unpacking GEMV at K = 5120 and 17408; at K = 6144 and 10240 it
-  // walks the rows with its long-row kernel and this path is faster (N = 5120, K = 6144:
-  // 7.7 against 8.1 us)
-  if (a.M == 1 && a.mode == MXFP8 && (a.K == 5120 || g.P == 3)) return false;
+  // mxfp8 at M = 1: the unpacking GEMV at K = 5120, where it decodes at 1 VALU op per
+  // weight byte and streams faster; past K = 5120 it walks the rows with its long-row
+  // kernel and this path is faster (N = 5120: 7.7 against 8.1 us at K = 6144, 15.75
+  // against 17.0 at K = 17408)
+  if (a.M == 1 && a.mode == MXFP8 && a.K == 5120) return false;
   if (a.N < 4096) return false;
   // several passes keep every row block's partial sums in LDS
   if (g.P > 1 && (qf_cus() == 0 || qf_flush_rows(a, qf_nrb(a, qf_cus())) < qf_nrb(a, qf_cus()))) return false;
