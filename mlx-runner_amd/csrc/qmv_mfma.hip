@@ -197,9 +197,9 @@ constexpr size_t qf_lds_bytes(int M, int Q, int F) {
 // re-read the range's last row for output rows that are dropped; their tile rows keep
 // stale bytes, which reach only those rows).
 //
-// SL > 0 (nvfp4, one unit in flight, one pass, every workgroup the same 3 or more row
-// blocks, the last of at most 4 SL rows per matrix): likewise for the last row block, with
-// the loop's last two steps unrolled after it.
+// SL > 0 (one unit in flight, one pass, every workgroup the same 3 or more row blocks, the
+// last of at most SL loads' rows per matrix): likewise for the last row block, with the
+// loop's last two steps unrolled after it.
 template <int MODE, int M, int Q, int NMAT, int D, int P, bool PARTS = false, int S1 = 0, int SL = 0>
 __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, int rbase, int rrem,
                                                           const uint16_t *__restrict__ x,
@@ -268,8 +268,7 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
     return a;
   };
   static_assert(S1 == 0 || (NMAT == 1 && D == 1 && S1 < G::LOADS), "short row block");
-  static_assert(SL == 0 || (MODE == NVFP4 && D == 1 && P == 1 && !PARTS && S1 == 0 && SL < G::LOADS / NMAT),
-                "short last row block");
+  static_assert(SL == 0 || (D == 1 && P == 1 && !PARTS && S1 == 0 && SL < G::LOADS / NMAT), "short last row block");
   // load i of a unit whose rows are at most NL loads' worth per matrix (NL = G::LOADS: all)
   auto load_on = [](int i, int nl) { return (NMAT == 2 ? i % (G::LOADS / 2) : i) < nl; };
   using AllLoads = std::integral_constant<int, G::LOADS>;
@@ -979,14 +978,14 @@ static hipError_t launch_qf(const QmmArgs &a, const uint8_t *w2, const uint8_t *
   return hipGetLastError();
 }
 
-// nvfp4 loads (4 rows each, per matrix) of the last row block of RB-row blocks when every
+// Loads (of RPL rows each, per matrix) of the last row block of RB-row blocks when every
 // workgroup has the same min_nb or more row blocks and the last is short; 0 otherwise.
-static int qf_short_last(const QmmArgs &a, int grid, int RB, int min_nb = 3) {
+static int qf_short_last(const QmmArgs &a, int grid, int RB, int min_nb = 3, int RPL = 4) {
   const int rmin = a.N / grid, rmax = rmin + (a.N % grid ? 1 : 0);
   const int nb = (rmax + RB - 1) / RB;
   if (nb < min_nb || (rmin + RB - 1) / RB != nb) return 0;
-  const int sl = (rmax - RB * (nb - 1) + 3) / 4;
-  return sl < RB / 4 ? sl : 0;
+  const int sl = (rmax - RB * (nb - 1) + RPL - 1) / RPL;
+  return sl < RB / RPL ? sl : 0;
 }
 
 // One unit in flight per wave at every size.  (Two, once the rule for ranges of 1-4 row
@@ -1050,6 +1049,13 @@ static hipError_t launch_qf_d(const QmmArgs &a, const uint8_t *w2, const uint8_t
     } else {
       if (sl == 1) return launch_qf<MODE, M, 10, NMAT, 1, 1, false, 0, 1>(a, w2, s2, grid, F, st);
     }
+  }
+  // mxfp8 (the model's shapes: 2, 4 or 5 of 8 loads; the MLP form measured no faster)
+  if constexpr (MODE == MXFP8 && NMAT == 1 && !PARTS && M <= 8) {
+    const int sl = qf_short_last(a, grid, 16, 3, 2);
+    if (sl == 2) return launch_qf<MODE, M, 10, NMAT, 1, 1, false, 0, 2>(a, w2, s2, grid, F, st);
+    if (sl == 4) return launch_qf<MODE, M, 10, NMAT, 1, 1, false, 0, 4>(a, w2, s2, grid, F, st);
+    if (sl == 5) return launch_qf<MODE, M, 10, NMAT, 1, 1, false, 0, 5>(a, w2, s2, grid, F, st);
   }
   return launch_qf<MODE, M, 10, NMAT, 1, 1, PARTS>(a, w2, s2, grid, F, st);
 }

@@ -410,7 +410,8 @@ def make_x(rng, M, K, kind):
                                       ("nvfp4", 1, 17408), ("nvfp4", 2, 17408), ("nvfp4", 3, 17408),
                                       ("nvfp4", 3, 10240), ("nvfp4", 4, 12288), ("nvfp4", 2, 5120),
                                       ("nvfp4", 2, 6144), ("mxfp8", 2, 5120), ("mxfp8", 4, 6144),
-                                      ("mxfp8", 8, 5120)])
+                                      ("mxfp8", 8, 5120), ("mxfp8", 2, 17408), ("mxfp8", 3, 10240),
+                                      ("mxfp8", 8, 17408)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
 def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
     K = 5120
