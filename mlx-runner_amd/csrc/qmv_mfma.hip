@@ -936,10 +936,15 @@ bool qmv_mfma_ok(const QmmArgs &a) {
   // x of every pass is held in registers: 6-8 rows fit two passes, 9-16 rows one
   if ((a.M > 5 && g.P == 3) || (a.M > 8 && g.P > 1)) return false;
   // Where this path is faster than the unpacking GEMV (measured on the 256-CU
-  // MI355X): nvfp4 at M = 1 with many rows per CU at K = 5120 (it pays a per-workgroup
-  // x split and pipeline fill) and at K = 17408 (N = 5120: 11.8 against 12.4 us).
-  // At M >= 2 from N = 4096.
-  if (a.M == 1 && a.mode == NVFP4 && g.P == 1 && a.N < 16384) return false;
+  // MI355X): nvfp4 at M = 1 at K = 17408 (N = 5120: 11.8 against 12.4 us) and at one
+  // pass from N = 4096, except with 17-24 rows per workgroup (two row blocks, the second
+  // short: 5120 x 5120 4.7 against 5.3 us, 6144 x 5120 5.2 against 5.4, 5120 x 6144 5.2
+  // against 5.3; 12288 x 5120 7.0 against 7.9, 10240 x 5120 6.5 against 7.1, the q+k+v
+  // group of 14336 rows 8.3 against 8.9).  At M >= 2 from N = 4096.
+  if (a.M == 1 && a.mode == NVFP4 && g.P == 1 && qf_cus() > 0) {
+    const int rmax = (a.N + qf_cus() - 1) / qf_cus();
+    if (rmax > 16 && rmax <= 24) return false;
+  }
   // mxfp8 at M = 1: the unpacking GEMV at K = 5120, where it decodes at 1 VALU op per
   // weight byte and streams faster; past K = 5120 it walks the rows with its long-row
   // kernel and this path is faster (N = 5120: 7.7 against 8.1 us at K = 6144, 15.75

@@ -388,8 +388,8 @@ def make_x(rng, M, K, kind):
     return bf16(x)
 
 
-# Shapes above the MFMA decode path's thresholds (K = 5120: nvfp4 M = 1 from
-# N = 16384, M >= 2 from N = 4096): ragged row blocks (N % 16 != 0), and a row
+# Shapes above the MFMA decode path's thresholds (K = 5120: from N = 4096, nvfp4 M = 1
+# not at 17-24 rows per workgroup): ragged row blocks (N % 16 != 0), and a row
 # range per workgroup long enough (N = 70001) to need several partial-sum flushes.
 # nvfp4 M = 3-4 runs the 32x32x64 form (32-row blocks, flushes every 4 blocks);
 # mxfp8 M = 5-8 the 16x16x128 form with all 16 A columns (8 rows x hi|lo) live, M = 9-16
@@ -411,7 +411,8 @@ def make_x(rng, M, K, kind):
                                       ("nvfp4", 3, 10240), ("nvfp4", 4, 12288), ("nvfp4", 2, 5120),
                                       ("nvfp4", 2, 6144), ("mxfp8", 2, 5120), ("mxfp8", 4, 6144),
                                       ("mxfp8", 8, 5120), ("mxfp8", 2, 17408), ("mxfp8", 3, 10240),
-                                      ("mxfp8", 8, 17408)])
+                                      ("mxfp8", 8, 17408), ("nvfp4", 1, 4096), ("nvfp4", 1, 10240),
+                                      ("nvfp4", 1, 12288)])
 @pytest.mark.parametrize("xkind", ["normal", "edge"])
 def test_decode_mfma_shapes_match_oracle(mode, M, N, xkind):
     K = 5120
