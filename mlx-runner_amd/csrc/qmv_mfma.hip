@@ -370,9 +370,12 @@ __global__ __launch_bounds__(64 * Q) void qmv_mfma_kernel(int N, int K, int F, i
       if (row < r_end) {
         // (the part lookup only in the grouped instances: it costs registers in the loop)
         const uint16_t v = f32_to_bf16_rne(out);
-        if constexpr (PARTS)
+        if constexpr (PARTS) {
+          // x of one row leaves n0 unused; kept live here, its SGPR is not reused early
+          // (a reuse made the first weight loads wait for the s_load of the part table)
+          if constexpr (M == 1) asm volatile("" ::"s"(yo.n0));
           *yo.at(m, row) = v;
-        else
+        } else
           yo.y0[(int64_t)m * N + row] = v;
       }
     }
